@@ -1,0 +1,255 @@
+"""Benchmark of the packed-KV hot path on one MI355X.
+
+Headline (`value`): pack throughput on the whole-volume pack workload
+(32 layers x 5 KV heads x 6144 tokens of bf16 K and V, 96 frame tiles of 64 tokens with
+seeded 4/8/16-bit widths), in algorithmic GB/s = (bytes read + bytes written) / time.
+Also reported on the same line: frame-chunk attention (15 Q / 5 KV heads, 64-token
+causal chunk over 1024/4096/8128-token mixed histories) in us/layer, GB/s and TFLOP/s;
+candidate scoring (4 continuations of 8-24 tokens over a 6144-token 4-bit / 8-bit
+history); and the reference CPU path timed on this host (the oracle restatement).
+
+Attention timings rotate over distinct per-layer histories whose total exceeds the
+256 MB Infinity Cache, so the history is read from HBM.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, 'dynamic-kv-cache_amd'))
+sys.path.insert(0, REPO)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+LAYERS, HEADS, Q_HEADS, TILE = 32, 5, 15, 64
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument('--gpus', type=int, default=1)
+    p.add_argument('--steps', type=int, default=200)
+    p.add_argument('--warmup', type=int, default=20)
+    p.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
+    p.add_argument('--only', choices=['pack', 'attn', 'cand', 'all'], default='all')
+    p.add_argument('--rotate', type=int, default=48, help='distinct layers attention rotates over')
+    return p.parse_args()
+
+
+def time_launches(fn, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    end.synchronize()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms per launch
+
+
+def pack_bytes(bits, layers=LAYERS, heads=HEADS, tile=TILE):
+    rows_per_frame = layers * 2 * heads * tile
+    read = rows_per_frame * 128 * len(bits)
+    write = sum(rows_per_frame * {4: 40, 8: 72, 16: 128}[b] for b in bits)
+    return read, write
+
+
+def bench_pack(steps, warmup):
+    import torch
+    from dkv.gpu_cache import GPUCache
+    from dkv.workloads import pack_volume
+    vol = pack_volume(seed=0, layers=LAYERS, frames=96)
+    dev = torch.device('cuda:0')
+    k, v = vol['k'].to(dev), vol['v'].to(dev)
+    cache = GPUCache(None, layers=LAYERS, heads=HEADS, max_tokens=96 * TILE)
+    batch = cache.append_batch(k, v, vol['bits'], [TILE] * 96)
+    ms = time_launches(batch.run, steps, warmup)
+    read, write = pack_bytes(vol['bits'])
+    gbs = (read + write) / (ms * 1e-3) / 1e9
+    return dict(ms=ms, gbs=gbs, read_bytes=read, write_bytes=write, bits=vol['bits'])
+
+
+def attention_setup(past, rotate, bits, nq=64, segments=None, seed=0):
+    """`rotate` layers, each with its own copy of one seeded history; returns launchers."""
+    import ctypes
+    import torch
+    from dkv import _lib
+    from dkv.gpu_cache import GPUCache
+    from dkv.workloads import outlier_values
+    dev = torch.device('cuda:0')
+    g = torch.Generator().manual_seed(seed)
+    hk = outlier_values((HEADS, past, 64), g, 0).to(dev)
+    hv = outlier_values((HEADS, past, 64), g, 0).to(dev)
+    q = outlier_values((Q_HEADS, nq, 64), g, 0).to(dev)[None]
+    kn = outlier_values((HEADS, nq, 64), g, 0).to(dev)[None]
+    vn = outlier_values((HEADS, nq, 64), g, 0).to(dev)[None]
+    cache = GPUCache(None, layers=rotate, heads=HEADS, max_tokens=past + nq)
+    tiles = (past + TILE - 1) // TILE
+    lengths = [min(TILE, past - TILE * i) for i in range(tiles)]
+    cache.append_batch(hk[None].expand(rotate, -1, -1, -1).contiguous(),
+                       hv[None].expand(rotate, -1, -1, -1).contiguous(), bits, lengths)
+    cache.select(16)
+    for layer in range(rotate):
+        cache.append(kn, vn, layer)
+    out = torch.empty((1, nq, Q_HEADS, 64), dtype=torch.bfloat16, device=dev)
+    lib = _lib.load()
+    args = [cache.attend_args(q, kn, vn, layer, past, out, segments) for layer in range(rotate)]
+    need = lib.dkv_attend_workspace_bytes(ctypes.byref(args[0]))
+    ws = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+    for a in args:
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    stream = _lib.stream_handle(dev)
+    refs = [ctypes.byref(a) for a in args]
+    state = {'i': 0}
+
+    def launch():
+        i = state['i']
+        rc = lib.dkv_attend(refs[i], stream)
+        if rc:
+            _lib.check(rc, 'dkv_attend')
+        state['i'] = (i + 1) % rotate
+    hist_bytes = sum(HEADS * 2 * n * {4: 40, 8: 72, 16: 128}[b] for b, n in zip(bits, lengths))
+    chunk_bytes = (Q_HEADS * nq * 64 * 2) * 2 + HEADS * nq * 64 * 2 * 2  # q + out, k_new + v_new
+    return launch, hist_bytes + chunk_bytes, dict(cache=cache, keep=(hk, hv, q, kn, vn, out, ws, args))
+
+
+def attention_flops(past, lengths):
+    # 2 matmuls (QK^T and PV) of 2*64 flops per (q row, visible key), per Q head
+    visible = sum(n * past + n * (n + 1) // 2 for n in lengths)
+    return 4 * 64 * Q_HEADS * visible
+
+
+def bench_attention(past, steps, warmup, rotate):
+    from dkv.workloads import bit_schedule
+    bits = bit_schedule(past, (past + TILE - 1) // TILE)
+    launch, nbytes, keep = attention_setup(past, rotate, bits, seed=past)
+    ms = time_launches(launch, steps, warmup)
+    flops = attention_flops(past, [64])
+    del keep
+    return dict(us_per_layer=ms * 1e3, gbs=nbytes / (ms * 1e-3) / 1e9, tflops=flops / (ms * 1e-3) / 1e12,
+                bytes=nbytes, flops=flops, mfma_frac=flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS)
+
+
+def bench_candidates(bits, steps, warmup, rotate):
+    from dkv.workloads import candidate_lengths
+    lengths = candidate_lengths(0, 4)
+    bounds = [0]
+    for n in lengths:
+        bounds.append(bounds[-1] + n)
+    past = 6144
+    launch, nbytes, keep = attention_setup(past, rotate, [bits] * (past // TILE), nq=bounds[-1], segments=bounds,
+                                           seed=bits)
+    ms = time_launches(launch, steps, warmup)
+    flops = attention_flops(past, lengths)
+    del keep
+    return dict(us_per_batch=ms * 1e3, gbs=nbytes / (ms * 1e-3) / 1e9, tflops=flops / (ms * 1e-3) / 1e12,
+                bytes=nbytes, flops=flops, lengths=lengths, hbm_frac=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS)
+
+
+def cpu_baselines(target_s=8.0):
+    """The reference CPU path restated in torch on this host's cores (oracle; timed, not checked)."""
+    import torch
+    from dkv.workloads import frame_chunk_case, pack_volume
+    from oracle.cpu_path import MixedPrecisionCache, cpu_attention_step
+    from oracle.kv_quantization import pack
+    cores = torch.get_num_threads()
+    # Pack: 2 layers of the pack workload (1/16 of the volume), every tile packed as the CPU path does.
+    vol = pack_volume(seed=0, layers=2, frames=96)
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        for f, b in enumerate(vol['bits']):
+            for layer in range(2):
+                pack(vol['k'][layer:layer + 1, :, 64 * f:64 * f + 64], b)
+                pack(vol['v'][layer:layer + 1, :, 64 * f:64 * f + 64], b)
+        reps += 1
+        if time.perf_counter() - t0 > target_s / 2:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    read, write = pack_bytes(vol['bits'], layers=2)
+    pack_gbs = (read + write) / dt / 1e9
+    # Attention: the CPU path's per-layer update + SDPA for one 64-token frame over 8128 history tokens.
+    case = frame_chunk_case(8128, seed=8128)
+    c = MixedPrecisionCache()
+    for i, b in enumerate(case['bits']):
+        c.select(b)
+        c.update(case['k_hist'][None, :, 64 * i:64 * i + 64], case['v_hist'][None, :, 64 * i:64 * i + 64], 0)
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        c2 = MixedPrecisionCache()
+        c2.segments = {0: list(c.segments[0])}
+        c2.select(16)
+        cpu_attention_step(c2, case['q'][None], case['k_new'][None], case['v_new'][None])
+        reps += 1
+        if time.perf_counter() - t0 > target_s / 2:
+            break
+    attn_ms = (time.perf_counter() - t0) / reps * 1e3
+    return dict(pack_gbs=pack_gbs, attn_ms_per_layer_8128=attn_ms, cores=cores,
+                pack_sample='2 of 32 layers of the pack workload (96 tiles, K and V)',
+                attn_sample='one layer, 64-token frame over 8128 mixed history tokens (127 tiles)')
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps(dict(error='this build runs on one GPU; --gpus must be 1',
+                              detail='multi-GPU sharding is design-only (DESIGN.md)')), flush=True)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print(json.dumps(dict(error='no HIP device visible')), flush=True)
+        sys.exit(2)
+    from dkv import _lib
+    _lib.load()
+    res = {}
+    if args.only in ('pack', 'all'):
+        res['pack'] = bench_pack(args.steps, args.warmup)
+        print(f"# pack: {res['pack']['ms'] * 1e3:.1f} us/launch, {res['pack']['gbs']:.0f} GB/s", flush=True)
+    if args.only in ('attn', 'all'):
+        res['attention'] = {}
+        for past in (1024, 4096, 8128):
+            r = bench_attention(past, args.steps, args.warmup, args.rotate)
+            res['attention'][f'past_{past}'] = r
+            print(f"# attn past={past}: {r['us_per_layer']:.2f} us/layer, {r['gbs']:.0f} GB/s, "
+                  f"{r['tflops']:.1f} TFLOP/s", flush=True)
+    if args.only in ('cand', 'all'):
+        res['candidates'] = {}
+        for bits in (4, 8):
+            r = bench_candidates(bits, args.steps, args.warmup, args.rotate)
+            res['candidates'][f'{bits}bit'] = r
+            print(f"# candidates {bits}-bit: {r['us_per_batch']:.2f} us, {r['gbs']:.0f} GB/s", flush=True)
+    cpu = None if args.no_cpu else cpu_baselines()
+    p = res.get('pack')
+    line = dict(
+        metric='packed-KV attn us/layer + HBM GB/s @8k mixed history; pack GB/s; frames/s e2e',
+        value=round(p['gbs'], 2) if p else None, unit='GB/s', n_gpus=1, steps=args.steps, warmup=args.warmup,
+        ms_per_step=round(p['ms'], 5) if p else None, higher_is_better=True, scaling='weak', vs_baseline=None,
+        dtype='bf16->u4/u8/bf16', data='synthetic',
+        config=dict(workload='pack: 32 layers x 5 KV heads x 6144 tokens (96 tiles of 64) bf16 K+V, '
+                             'seeded 40/40/20 4/8/16-bit tiles, one launch', parallelism='none (1 GPU)'),
+    )
+    if p:
+        line['roofline'] = dict(bound='hbm', achieved=round(p['gbs'], 1), peak=HBM_PEAK_GBS,
+                                unit='GB/s', frac=round(p['gbs'] / HBM_PEAK_GBS, 4), traffic=None)
+    if 'attention' in res:
+        line['attention'] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in r.items()}
+                             for k, r in res['attention'].items()}
+    if 'candidates' in res:
+        line['candidates'] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in r.items()}
+                              for k, r in res['candidates'].items()}
+    if cpu:
+        line['cpu_baseline'] = dict(value=round(cpu['pack_gbs'], 4), unit='GB/s', cores=cpu['cores'], kind='port',
+                                    sample=cpu['pack_sample'],
+                                    attn_ms_per_layer_8128=round(cpu['attn_ms_per_layer_8128'], 3),
+                                    attn_sample=cpu['attn_sample'])
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == '__main__':
+    main()

@@ -1,0 +1,409 @@
+// Fused causal GQA attention over the packed arena (gfx950).
+//
+// Semantics (src/gpu_kernels.py:71-105, src/cache_manager.py:43-63): query row
+// m of Q head qh attends to every history token t < past of KV head
+// qh / (q_heads / heads), dequantized as q*s + a, and to the chunk's own native
+// K/V rows j <= m of its chunk segment. softmax(scale * q.k) weights V.
+//
+// Work split: a workgroup owns one KV head, one group of query rows (all GQA
+// heads of that KV head share each K/V tile) and one contiguous range of
+// "units" (history tiles, then 64-token pieces of the current chunk). With more
+// than one range per head, each workgroup writes unnormalized partial
+// (O, max, sum) and combine_kernel merges them with the usual log-sum-exp
+// rescaling. Softmax runs in base 2: x = score * scale * log2(e).
+#include "dkv_common.h"
+#include <math.h>
+
+namespace dkv {
+
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr int ATT_THREADS = 256;
+
+struct Unit {
+  // history tile: src rows come from the arena; chunk piece: from k_new/v_new
+  bool chunk;
+  int first;  // first logical token (history) or chunk row (chunk)
+  int valid;  // rows present in this unit
+  int bits;
+  const uint8_t* ksub;
+  const uint8_t* vsub;
+  int rows;  // rows of the tile (sub-block stride basis)
+};
+
+__device__ __forceinline__ Unit get_unit(const dkv_attn_args& a, int u) {
+  Unit un;
+  if (u < a.n_tiles) {
+    const dkv_tile t = a.tiles[u];
+    un.chunk = false;
+    un.first = t.token_start;
+    un.valid = min((int)t.rows, a.past - t.token_start);
+    un.bits = t.bits;
+    un.rows = t.rows;
+    const int64_t sb = subblock_bytes(t.rows, t.bits);
+    const uint8_t* base = static_cast<const uint8_t*>(a.arena) + t.offset;
+    const int h = blockIdx.y;
+    un.ksub = base + ((int64_t)(a.layer * 2 + 0) * a.heads + h) * sb;
+    un.vsub = base + ((int64_t)(a.layer * 2 + 1) * a.heads + h) * sb;
+  } else {
+    const int c = u - a.n_tiles;
+    un.chunk = true;
+    un.first = c * TILE;
+    un.valid = min(TILE, a.nq - c * TILE);
+    un.bits = 16;
+    un.rows = TILE;
+    un.ksub = un.vsub = nullptr;
+  }
+  return un;
+}
+
+// Chunk segment of chunk row j (one segment when n_segs <= 1).
+__device__ __forceinline__ int chunk_seg_start(const dkv_attn_args& a, int j) {
+  int start = 0;
+  for (int s = 1; s < a.n_segs; ++s)
+    if (j >= a.seg_bounds[s]) start = a.seg_bounds[s];
+  return start;
+}
+
+// Dequantizes 16 consecutive elements [c*16, c*16+16) of row r of a unit into
+// fp32 (q*s + a with separately rounded multiply and add).
+__device__ __forceinline__ void load_row16(const dkv_attn_args& a, const Unit& un, int kv, int r, int c,
+                                           float* x) {
+  if (un.chunk) {
+    const int j = un.first + r;
+    const uint16_t* src = kv == 0
+        ? static_cast<const uint16_t*>(a.k_new) + blockIdx.y * a.kn_head_stride + (int64_t)j * a.kn_tok_stride
+        : static_cast<const uint16_t*>(a.v_new) + blockIdx.y * a.vn_head_stride + (int64_t)j * a.vn_tok_stride;
+    const uint4* p = reinterpret_cast<const uint4*>(src + c * 16);
+    uint4 w0 = p[0], w1 = p[1];
+    uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      x[2 * i] = bf16_lo(w[i]);
+      x[2 * i + 1] = bf16_hi(w[i]);
+    }
+    return;
+  }
+  const uint8_t* sub = kv == 0 ? un.ksub : un.vsub;
+  const uint8_t* prow = sub + (int64_t)r * row_bytes(un.bits);
+  if (un.bits == 16) {
+    const uint4* p = reinterpret_cast<const uint4*>(prow + c * 32);
+    uint4 w0 = p[0], w1 = p[1];
+    uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      x[2 * i] = bf16_lo(w[i]);
+      x[2 * i + 1] = bf16_hi(w[i]);
+    }
+    return;
+  }
+  const float2 as = reinterpret_cast<const float2*>(sub + (int64_t)un.rows * row_bytes(un.bits))[r];
+  uint32_t code[16];
+  if (un.bits == 4) {
+    uint2 w = *reinterpret_cast<const uint2*>(prow + c * 8);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) code[i] = (w.x >> (4 * i)) & 15u;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) code[8 + i] = (w.y >> (4 * i)) & 15u;
+  } else {
+    uint4 w = *reinterpret_cast<const uint4*>(prow + c * 16);
+    uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) code[i] = (ww[i >> 2] >> (8 * (i & 3))) & 255u;
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) x[i] = __fadd_rn(__fmul_rn((float)code[i], as.y), as.x);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// Vector path: fp32 everywhere. A wave owns VEC_RPW query rows; lane n scores
+// token n of the unit, lane d accumulates output column d.
+constexpr int VEC_RPW = 16;
+constexpr int VEC_ROWS = 4 * VEC_RPW;  // rows per workgroup
+
+__global__ void __launch_bounds__(ATT_THREADS)
+attn_vec_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ part_o,
+                float2* __restrict__ part_ml) {
+  __shared__ float Qs[VEC_ROWS][D];
+  __shared__ float Kt[TILE][D + 1];
+  __shared__ float Vt[TILE][D];
+  __shared__ float Ps[4][TILE];
+
+  const int split = blockIdx.x, h = blockIdx.y, rg = blockIdx.z;
+  const int G = a.q_heads / a.heads;
+  const int R = G * a.nq;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int u0 = (int)((int64_t)units * split / splits);
+  const int u1 = (int)((int64_t)units * (split + 1) / splits);
+  const float xs = a.scale * LOG2E;
+
+  // Stage this group's query rows in LDS as fp32.
+  for (int idx = tid; idx < VEC_ROWS * (D / 8); idx += ATT_THREADS) {
+    const int rl = idx / (D / 8), c8 = idx % (D / 8);
+    const int r = rg * VEC_ROWS + rl;
+    float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (r < R) {
+      const int g = r / a.nq, m = r - g * a.nq;
+      const uint16_t* src = static_cast<const uint16_t*>(a.q) + (int64_t)(h * G + g) * a.q_head_stride +
+                            (int64_t)m * a.q_tok_stride + c8 * 8;
+      uint4 wq = *reinterpret_cast<const uint4*>(src);
+      uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[2 * i] = bf16_lo(ww[i]);
+        v[2 * i + 1] = bf16_hi(ww[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) Qs[rl][c8 * 8 + i] = v[i];
+  }
+
+  float acc[VEC_RPW], mx[VEC_RPW], sm[VEC_RPW];
+#pragma unroll
+  for (int i = 0; i < VEC_RPW; ++i) {
+    acc[i] = 0.f;
+    mx[i] = -INFINITY;
+    sm[i] = 0.f;
+  }
+
+  for (int u = u0; u < u1; ++u) {
+    const Unit un = get_unit(a, u);
+    __syncthreads();  // previous unit's readers are done; Qs is staged
+    {
+      const int r = tid >> 2, c = tid & 3;
+      float xk[16], xv[16];
+      if (r < un.valid) {
+        load_row16(a, un, 0, r, c, xk);
+        load_row16(a, un, 1, r, c, xv);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) xk[i] = xv[i] = 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        Kt[r][c * 16 + i] = xk[i];
+        Vt[r][c * 16 + i] = xv[i];
+      }
+    }
+    __syncthreads();
+    const int j = un.first + lane;  // chunk row of this lane's token (chunk units)
+    const int jseg = un.chunk ? chunk_seg_start(a, j) : 0;
+#pragma unroll
+    for (int i = 0; i < VEC_RPW; ++i) {
+      const int rl = w * VEC_RPW + i;
+      const int r = rg * VEC_ROWS + rl;
+      if (r >= R) break;  // wave-uniform
+      const int m = r % a.nq;
+      bool vis = lane < un.valid;
+      if (un.chunk) vis = vis && j <= m && jseg == chunk_seg_start(a, m);
+      float s = 0.f;
+#pragma unroll 16
+      for (int d = 0; d < D; ++d) s = fmaf(Qs[rl][d], Kt[lane][d], s);
+      const float x = vis ? s * xs : -INFINITY;
+      const float tmax = wave_max(x);
+      if (tmax == -INFINITY) continue;  // wave-uniform: nothing visible here
+      const float mnew = fmaxf(mx[i], tmax);
+      const float alpha = exp2f(mx[i] - mnew);
+      const float p = vis ? exp2f(x - mnew) : 0.f;
+      sm[i] = sm[i] * alpha + wave_sum(p);
+      mx[i] = mnew;
+      Ps[w][lane] = p;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      float o = acc[i] * alpha;
+#pragma unroll 16
+      for (int n = 0; n < TILE; ++n) o = fmaf(Ps[w][n], Vt[n][lane], o);
+      acc[i] = o;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+  }
+
+  // Epilogue: final output (one split) or partials.
+#pragma unroll
+  for (int i = 0; i < VEC_RPW; ++i) {
+    const int r = rg * VEC_ROWS + w * VEC_RPW + i;
+    if (r >= R) break;
+    if (splits == 1) {
+      const int g = r / a.nq, m = r - g * a.nq;
+      const float o = acc[i] / sm[i];
+      const int64_t off = (int64_t)m * a.out_tok_stride + (int64_t)(h * G + g) * a.out_head_stride + lane;
+      if (a.out_dtype == 1) static_cast<float*>(a.out)[off] = o;
+      else static_cast<uint16_t*>(a.out)[off] = (uint16_t)f32_to_bf16_rne(o);
+    } else {
+      const int64_t base = ((int64_t)h * splits + split) * R + r;
+      part_o[base * D + lane] = acc[i];
+      if (lane == 0) part_ml[base] = make_float2(mx[i], sm[i]);
+    }
+  }
+}
+
+// Log-sum-exp merge of split partials: one thread per (row, column).
+__global__ void __launch_bounds__(256)
+combine_kernel(dkv_attn_args a, int splits, const float* __restrict__ part_o,
+               const float2* __restrict__ part_ml) {
+  const int h = blockIdx.y;
+  const int G = a.q_heads / a.heads;
+  const int R = G * a.nq;
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  const int r = idx >> 6, d = idx & 63;
+  if (r >= R) return;
+  const int64_t base = (int64_t)h * splits * R + r;
+  float M = -INFINITY;
+  for (int s = 0; s < splits; ++s) M = fmaxf(M, part_ml[base + (int64_t)s * R].x);
+  float L = 0.f, O = 0.f;
+  for (int s = 0; s < splits; ++s) {
+    const float2 ml = part_ml[base + (int64_t)s * R];
+    if (ml.x == -INFINITY) continue;
+    const float f = exp2f(ml.x - M);
+    L = fmaf(ml.y, f, L);
+    O = fmaf(part_o[(base + (int64_t)s * R) * D + d], f, O);
+  }
+  const float o = O / L;
+  const int g = r / a.nq, m = r - g * a.nq;
+  const int64_t off = (int64_t)m * a.out_tok_stride + (int64_t)(h * G + g) * a.out_head_stride + d;
+  if (a.out_dtype == 1) static_cast<float*>(a.out)[off] = o;
+  else static_cast<uint16_t*>(a.out)[off] = (uint16_t)f32_to_bf16_rne(o);
+}
+
+// ---------------------------------------------------------------------------
+// Host side.
+
+struct Plan {
+  int path;        // 1 vector, 2 MFMA
+  int units;
+  int splits;
+  int row_groups;
+  int rows_per_group;
+  int64_t part_o_bytes, part_ml_bytes;
+};
+
+static int num_cus() {
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+  }
+  return cus;
+}
+
+static int check_args(const dkv_attn_args& a) {
+  if (!a.q || !a.k_new || !a.v_new || !a.out || (a.n_tiles > 0 && (!a.tiles || !a.arena))) {
+    set_error("dkv_attend: null pointer argument");
+    return DKV_EINVAL;
+  }
+  if (a.heads <= 0 || a.q_heads <= 0 || a.q_heads % a.heads || a.nq <= 0 || a.past < 0 ||
+      a.n_tiles < 0 || a.layer < 0 || a.layer >= a.layers) {
+    set_error("dkv_attend: bad shape (heads %d, q_heads %d, nq %d, past %d, layer %d/%d)", a.heads,
+              a.q_heads, a.nq, a.past, a.layer, a.layers);
+    return DKV_EINVAL;
+  }
+  if (a.n_segs < 0 || a.n_segs > DKV_MAX_CHUNK_SEGS) {
+    set_error("dkv_attend: n_segs %d outside [0, %d]", a.n_segs, DKV_MAX_CHUNK_SEGS);
+    return DKV_EINVAL;
+  }
+  if (a.n_segs > 1) {
+    if (a.seg_bounds[0] != 0 || a.seg_bounds[a.n_segs] != a.nq) {
+      set_error("dkv_attend: segment bounds must start at 0 and end at nq");
+      return DKV_EINVAL;
+    }
+    for (int s = 0; s < a.n_segs; ++s)
+      if (a.seg_bounds[s + 1] <= a.seg_bounds[s]) {
+        set_error("dkv_attend: segment bounds must increase");
+        return DKV_EINVAL;
+      }
+  }
+  if (a.out_dtype != 0 && a.out_dtype != 1) {
+    set_error("dkv_attend: out_dtype must be 0 (bf16) or 1 (fp32)");
+    return DKV_EINVAL;
+  }
+  auto a16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  if (!a16(a.q) || !a16(a.k_new) || !a16(a.v_new) || (a.q_head_stride & 7) || (a.q_tok_stride & 7) ||
+      (a.kn_head_stride & 7) || (a.kn_tok_stride & 7) || (a.vn_head_stride & 7) || (a.vn_tok_stride & 7)) {
+    set_error("dkv_attend: Q/K/V must be 16-byte aligned with strides that are multiples of 8 elements");
+    return DKV_EINVAL;
+  }
+  return 0;
+}
+
+static Plan make_plan(const dkv_attn_args& a) {
+  Plan p;
+  const int G = a.q_heads / a.heads;
+  const int R = G * a.nq;
+  p.path = 1;
+  p.rows_per_group = VEC_ROWS;
+  p.row_groups = (R + p.rows_per_group - 1) / p.rows_per_group;
+  p.units = a.n_tiles + (a.nq + TILE - 1) / TILE;
+  int splits = a.splits;
+  if (splits <= 0) {
+    const int target = 2 * num_cus();
+    const int per = a.heads * p.row_groups;
+    splits = (target + per - 1) / per;
+  }
+  if (splits > p.units) splits = p.units;
+  if (splits < 1) splits = 1;
+  p.splits = splits;
+  if (splits > 1) {
+    p.part_o_bytes = (int64_t)a.heads * splits * R * D * 4;
+    p.part_ml_bytes = (int64_t)a.heads * splits * R * 8;
+  } else {
+    p.part_o_bytes = p.part_ml_bytes = 0;
+  }
+  return p;
+}
+
+}  // namespace dkv
+
+using namespace dkv;
+
+extern "C" {
+
+int64_t dkv_attend_workspace_bytes(const dkv_attn_args* args) {
+  if (!args || args->heads <= 0 || args->q_heads <= 0 || args->q_heads % args->heads || args->nq <= 0)
+    return 0;
+  const Plan p = make_plan(*args);
+  return p.part_o_bytes + p.part_ml_bytes;
+}
+
+int dkv_attend(const dkv_attn_args* args, void* stream) {
+  clear_error();
+  if (!args) {
+    set_error("dkv_attend: null args");
+    return DKV_EINVAL;
+  }
+  const dkv_attn_args& a = *args;
+  if (int rc = check_args(a)) return rc;
+  const Plan p = make_plan(a);
+  const int64_t need = p.part_o_bytes + p.part_ml_bytes;
+  if (need > 0 && (!a.workspace || a.workspace_bytes < need)) {
+    set_error("dkv_attend: workspace of %lld bytes needed, %lld given", (long long)need,
+              (long long)a.workspace_bytes);
+    return DKV_EINVAL;
+  }
+  float* part_o = static_cast<float*>(a.workspace);
+  float2* part_ml = reinterpret_cast<float2*>(static_cast<char*>(a.workspace) + p.part_o_bytes);
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(attn_vec_kernel, dim3(p.splits, a.heads, p.row_groups), dim3(ATT_THREADS), 0, s, a,
+                     p.units, p.splits, part_o, part_ml);
+  if (p.splits > 1) {
+    const int R = (a.q_heads / a.heads) * a.nq;
+    hipLaunchKernelGGL(combine_kernel, dim3((R * D + 255) / 256, a.heads), dim3(256), 0, s, a, p.splits,
+                       part_o, part_ml);
+  }
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"

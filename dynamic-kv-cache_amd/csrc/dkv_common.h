@@ -1,0 +1,46 @@
+// Shared device/host helpers of libdkv: arena geometry, bf16 bit conversions,
+// argument checking and the thread-local error message.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "dkv.h"
+
+namespace dkv {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int D = DKV_HEAD_DIM;      // elements per (token, head) row
+constexpr int TILE = DKV_TILE_TOKENS;  // tokens per tile
+
+__host__ __device__ inline int64_t row_bytes(int bits) {
+  return bits == 4 ? 32 : (bits == 8 ? 64 : 128);
+}
+
+// One (layer, kv, head) sub-block of a tile: payload rows, then (a, s) fp32
+// pairs for 4/8-bit, rounded up to 16 bytes so every row and every sub-block
+// start is 128-bit aligned.
+__host__ __device__ inline int64_t subblock_bytes(int rows, int bits) {
+  int64_t b = (int64_t)rows * row_bytes(bits) + (bits < 16 ? (int64_t)rows * 8 : 0);
+  return (b + 15) & ~int64_t(15);
+}
+
+__host__ __device__ inline int64_t slab_bytes(int rows, int bits, int layers, int heads) {
+  return subblock_bytes(rows, bits) * (int64_t)layers * 2 * heads;
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// fp32 -> bf16 bits, round to nearest even (finite inputs; NaN stays NaN).
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// Thread-local message for DKV_EINVAL returns.
+void set_error(const char* fmt, ...);
+void clear_error();
+
+}  // namespace dkv

@@ -1,0 +1,60 @@
+"""Builds libdkv.so (the HIP kernels and their C ABI) for gfx950 with hipcc.
+
+Flags that matter for results:
+  -ffp-contract=off                          no silent FMA contraction: the
+                                             pack arithmetic and the q*s + a
+                                             dequantization round like the
+                                             reference's separate torch ops
+  -fhip-fp32-correctly-rounded-divide-sqrt   IEEE fp32 division in the pack
+  -Xclang -target-feature -Xclang -packed-fp32-ops
+                                             no packed fp32 VALU instructions
+"""
+import os
+import shutil
+import subprocess
+import sys
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG_DIR)  # dynamic-kv-cache_amd/
+REPO = os.path.dirname(ROOT)
+CSRC = os.path.join(ROOT, 'csrc')
+INCLUDE = os.path.join(REPO, 'include')
+LIB_NAME = 'libdkv.so'
+LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
+ARCH = os.environ.get('DKV_OFFLOAD_ARCH', 'gfx950')
+
+HIPCC_FLAGS = [
+    f'--offload-arch={ARCH}', '-O3', '-std=c++17', '-fPIC', '-shared',
+    '-ffp-contract=off', '-fhip-fp32-correctly-rounded-divide-sqrt',
+    '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
+    '-Wno-unused-command-line-argument',
+]
+
+
+def sources():
+    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith('.hip'))
+
+
+def hipcc():
+    path = shutil.which('hipcc') or '/opt/rocm/bin/hipcc'
+    if not os.path.exists(path):
+        raise RuntimeError('hipcc not found: libdkv needs ROCm to build')
+    return path
+
+
+def build(verbose=False, extra=()):
+    """Compiles every csrc/*.hip into one shared library next to this file."""
+    tmp = LIB_PATH + '.tmp'
+    cmd = [hipcc(), *HIPCC_FLAGS, *extra, '-I', INCLUDE, '-I', CSRC, '-o', tmp, *sources()]
+    if verbose:
+        print(' '.join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        sys.stderr.write(proc.stdout + proc.stderr)
+        raise RuntimeError(f'hipcc failed with status {proc.returncode}')
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == '__main__':
+    print(build(verbose=True))

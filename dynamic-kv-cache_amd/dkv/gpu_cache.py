@@ -1,0 +1,446 @@
+"""Packed mixed-precision KV cache on one preallocated HBM arena.
+
+Drop-in for the reference's GPUCache / install_packed_attention
+(src/gpu_cache.py:10-183): same constructor, methods, return values, errors and
+de-facto public attributes (seen, host_counts, backend, caps, codes, rows,
+plan). The storage underneath is different: instead of three per-precision
+pools with a per-token row map, every append at layer 0 opens a segment of
+64-token tiles in one byte arena, and a device tile table records each tile's
+offset, first token, rows and bit width. Pack, attention and reconstruct are
+hand-written HIP kernels reached through libdkv's C ABI (include/dkv.h).
+"""
+import bisect
+import ctypes
+import types
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+
+try:  # the reference subclasses transformers' DynamicCache; keep isinstance() working
+    from transformers.cache_utils import DynamicCache as _CacheBase
+except Exception:  # transformers absent: a plain object base keeps the kernels usable
+    _CacheBase = object
+
+TILE = 64
+BITS = (4, 8, 16)
+
+
+def row_bytes(bits):
+    return {4: 32, 8: 64, 16: 128}[bits]
+
+
+def subblock_bytes(rows, bits):
+    """Python mirror of dkv_subblock_bytes (include/dkv.h)."""
+    b = rows * row_bytes(bits) + (rows * 8 if bits < 16 else 0)
+    return (b + 15) & ~15
+
+
+def slab_bytes(rows, bits, layers, heads):
+    return subblock_bytes(rows, bits) * layers * 2 * heads
+
+
+def segment_bytes(rows, bits, layers, heads):
+    """Arena bytes of a segment of `rows` tokens: full tiles plus one partial."""
+    full, rem = divmod(rows, TILE)
+    return full * slab_bytes(TILE, bits, layers, heads) + (slab_bytes(rem, bits, layers, heads) if rem else 0)
+
+
+def worst_case_arena_bytes(tokens, layers, heads):
+    """Bytes that hold `tokens` tokens at any mix of widths and segment cuts."""
+    # 16-bit rows are the largest (128 B); each partial tile rounds up by < 16 B.
+    return layers * 2 * heads * (tokens * row_bytes(16) + 16 * tokens)
+
+
+class _Segment:
+    __slots__ = ('start', 'rows', 'bits', 'offset', 'tile0')
+
+    def __init__(self, start, rows, bits, offset, tile0):
+        self.start, self.rows, self.bits, self.offset, self.tile0 = start, rows, bits, offset, tile0
+
+    @property
+    def end(self):
+        return self.start + self.rows
+
+    @property
+    def ntiles(self):
+        return (self.rows + TILE - 1) // TILE
+
+
+class GPUCache(_CacheBase):
+    """Mixed 4/8/16-bit KV cache for batch one and head_dim 64 (src/gpu_cache.py:10-149)."""
+
+    def __init__(self, plan=None, layers=30, heads=3, dim=64, device='cuda', dtype=torch.bfloat16,
+                 backend='fused', block_m=16, block_n=64, max_tokens=8192, arena_bytes=None):
+        if _CacheBase is not object:
+            super().__init__()
+        if dim != 64:
+            raise ValueError('GPU kernel currently supports head_dim=64')
+        self.layers, self.heads, self.dim = layers, heads, dim
+        self.dtype, self.device = dtype, torch.device(device)
+        self.backend, self.block_m, self.block_n = backend, block_m, block_n
+        self.seen = [0] * layers
+        self.cursors = [0] * layers
+        self.pending_bits = 16
+        self.frame_id = -1
+        self.online = plan is None
+        self.plan = []  # (start, end, bits, row) per segment, as in the reference
+        self.segments = []
+        self.tile_starts = []  # first token of every tile, in token order
+        self.host_counts = {4: 0, 8: 0, 16: 0}
+        self.arena_used = 0
+        planned = []
+        for bits, n in (plan or []):
+            if bits not in self.host_counts or n < 0:
+                raise ValueError('Invalid GPU cache plan')
+            planned.append((bits, n))
+        if self.online:
+            self.capacity = max_tokens
+            need = worst_case_arena_bytes(max_tokens, layers, heads)
+            max_tiles = max_tokens
+        else:
+            self.capacity = sum(n for _, n in planned)
+            need = sum(segment_bytes(n, b, layers, heads) for b, n in planned if n)
+            max_tiles = sum((n + TILE - 1) // TILE for _, n in planned)
+        self.arena_bytes = int(arena_bytes) if arena_bytes is not None else max(need, 256)
+        self.arena = torch.empty(self.arena_bytes, dtype=torch.uint8, device=self.device)
+        self.tiles = torch.zeros((max(max_tiles, 1), 16), dtype=torch.uint8, device=self.device)
+        self._workspace = None
+        for bits, n in planned:
+            if n:
+                self._open_segment(self.segments[-1].end if self.segments else 0, n, bits)
+
+    # -- bookkeeping -------------------------------------------------------
+    def _open_segment(self, start, n, bits):
+        need = segment_bytes(n, bits, self.layers, self.heads)
+        if self.arena_used + need > self.arena_bytes:
+            self._grow(self.arena_used + need)
+        tile0 = len(self.tile_starts)
+        if tile0 + (n + TILE - 1) // TILE > self.tiles.shape[0]:
+            raise ValueError('GPU context limit exceeded')
+        seg = _Segment(start, n, bits, self.arena_used, tile0)
+        self.segments.append(seg)
+        self.tile_starts.extend(range(start, start + n, TILE))
+        self.plan.append((start, start + n, bits, self.host_counts[bits]))
+        self.host_counts[bits] += n
+        self.arena_used += need
+        return seg
+
+    def _grow(self, needed):
+        """Grows this cache's arena (forks keep theirs), like the reference's reserve()."""
+        size = max(needed, ((int(self.arena_bytes * 1.5) + 255) // 256) * 256)
+        target = torch.empty(size, dtype=torch.uint8, device=self.device)
+        if self.arena_used:
+            target[:self.arena_used].copy_(self.arena[:self.arena_used])
+        self.arena, self.arena_bytes = target, size
+
+    def reserve(self, bits, needed):
+        """Makes room for `needed` rows of width `bits` in total (src/gpu_cache.py:44-59)."""
+        more = needed - self.host_counts[bits]
+        if more <= 0:
+            return
+        extra = segment_bytes(more, bits, self.layers, self.heads) + 16 * self.layers * 2 * self.heads
+        if self.arena_used + extra > self.arena_bytes:
+            self._grow(self.arena_used + extra)
+
+    @property
+    def caps(self):
+        """Rows of each width the arena could hold (the reference's pool capacities)."""
+        per = self.layers * 2 * self.heads
+        return {b: self.arena_bytes // (per * (row_bytes(b) + (8 if b < 16 else 0))) for b in BITS}
+
+    @property
+    def codes(self):
+        """Per-token bit width, uint8 on the device (the reference's precision map)."""
+        out = torch.empty(self.capacity, dtype=torch.uint8)
+        for start, end, bits, _ in self.plan:
+            out[start:end] = bits
+        return out.to(self.device)
+
+    @property
+    def rows(self):
+        """Per-token row index within its width class (the reference's row map)."""
+        out = torch.empty(self.capacity, dtype=torch.int32)
+        for start, end, bits, row in self.plan:
+            out[start:end] = torch.arange(row, row + end - start, dtype=torch.int32)
+        return out.to(self.device)
+
+    def select(self, bits, frame_id=-1):
+        self.pending_bits, self.frame_id = bits, frame_id
+
+    def get_seq_length(self, layer_idx=0):
+        return self.seen[layer_idx]
+
+    def get_max_cache_shape(self, layer_idx=0):
+        return None
+
+    def __len__(self):
+        return self.layers
+
+    def _tiles_before(self, past):
+        return bisect.bisect_left(self.tile_starts, past)
+
+    # -- hot path ----------------------------------------------------------
+    @staticmethod
+    def _kv_view(x):
+        """[1, H, n, 64] view with contiguous rows, 16-byte aligned (copies otherwise)."""
+        if (x.stride(-1) != 1 or x.stride(1) % 8 or x.stride(2) % 8 or x.data_ptr() % 16
+                or x.dtype != torch.bfloat16):
+            x = x.to(torch.bfloat16).contiguous()
+        return x
+
+    def append(self, k, v, layer):
+        """Packs the new tokens of one layer; returns the history length (src/gpu_cache.py:68-94)."""
+        if k.shape[0] != 1 or k.shape[-1] != self.dim or k.device.type != 'cuda':
+            raise ValueError('GPU cache requires CUDA, batch one and the configured head dimension')
+        if k.dim() != 4 or k.shape[1] != self.heads or v.shape != k.shape or v.device != k.device:
+            raise ValueError(f'append expects k and v of shape [1, {self.heads}, n, {self.dim}]')
+        past = self.seen[layer]
+        n = k.shape[-2]
+        if past + n > self.capacity:
+            raise ValueError('GPU context limit exceeded')
+        write_tiles = 0
+        if self.online:
+            if layer == 0:
+                self._open_segment(past, n, self.pending_bits)
+                write_tiles = 1
+            seg = self.segments[-1] if self.segments else None
+        else:
+            cursor = self.cursors[layer]
+            while cursor < len(self.segments) and past >= self.segments[cursor].end:
+                cursor += 1
+            self.cursors[layer] = cursor
+            seg = self.segments[cursor] if cursor < len(self.segments) else None
+            if seg is not None and layer == 0 and past == seg.start:
+                write_tiles = 1
+        if seg is None or past + n > seg.end or seg.bits != self.pending_bits:
+            raise ValueError(f'Cache append does not match plan at token {past}, length {n}, bits {self.pending_bits}')
+        if n:
+            k, v = self._kv_view(k), self._kv_view(v)
+            job = _lib.PackJob(k.data_ptr(), v.data_ptr(), k.stride(1), k.stride(2), v.stride(1), v.stride(2),
+                               seg.offset, seg.rows, seg.start, past - seg.start, n, layer, seg.bits,
+                               seg.tile0, write_tiles)
+            lib = _lib.load()
+            _lib.check(lib.dkv_pack(ctypes.byref(job), self.arena.data_ptr(), self.arena_bytes,
+                                    self.tiles.data_ptr(), self.layers, self.heads,
+                                    _lib.stream_handle(self.device)), 'dkv_pack')
+        self.seen[layer] = past + n
+        return past
+
+    def append_batch(self, k, v, bits, lengths):
+        """Appends several segments for every layer in one pack launch.
+
+        k, v: [layers, heads, sum(lengths), 64] bf16 device tensors (last dim contiguous).
+        bits, lengths: width and token count of each segment, in order. Equivalent to calling
+        select(bits[i]) and append() for every layer and segment; returns the history length
+        before the batch. Returns a PackBatch that can re-run the same launch (benchmarks).
+        """
+        if k.shape[0] != self.layers or k.shape[1] != self.heads or k.shape[-1] != self.dim or k.device.type != 'cuda':
+            raise ValueError('append_batch expects [layers, heads, tokens, 64] CUDA tensors')
+        if sum(lengths) != k.shape[2] or len(bits) != len(lengths) or len(set(self.seen)) != 1:
+            raise ValueError('append_batch: lengths must cover the tokens and every layer must be level')
+        past = self.seen[0]
+        if past + k.shape[2] > self.capacity:
+            raise ValueError('GPU context limit exceeded')
+        k, v = self._kv_view4(k), self._kv_view4(v)
+        jobs = []
+        start = past
+        for b, n in zip(bits, lengths):
+            if self.online:
+                seg = self._open_segment(start, n, b)
+            else:
+                seg = next((s for s in self.segments if s.start <= start < s.end), None)
+                if seg is None or start + n > seg.end or seg.bits != b:
+                    raise ValueError(f'Cache append does not match plan at token {start}, length {n}, bits {b}')
+            for layer in range(self.layers):
+                t0 = start - past
+                jobs.append(_lib.PackJob(
+                    k[layer, :, t0:].data_ptr(), v[layer, :, t0:].data_ptr(), k.stride(1), k.stride(2),
+                    v.stride(1), v.stride(2), seg.offset, seg.rows, seg.start, start - seg.start, n, layer,
+                    seg.bits, seg.tile0, int(layer == 0 and start == seg.start)))
+            start += n
+        batch = PackBatch(self, jobs, max(lengths), keep=(k, v))
+        batch.run()
+        self.seen = [start] * self.layers
+        return batch
+
+    @staticmethod
+    def _kv_view4(x):
+        if (x.stride(-1) != 1 or x.stride(1) % 8 or x.stride(2) % 8 or x.stride(0) % 8 or x.data_ptr() % 16
+                or x.dtype != torch.bfloat16):
+            x = x.to(torch.bfloat16).contiguous()
+        return x
+
+    def attend_args(self, q, k, v, layer, past, out, segments=None, path=0, splits=0):
+        """Fills the C argument block of one attention call."""
+        nq = q.shape[-2]
+        a = _lib.AttnArgs()
+        a.q, a.q_head_stride, a.q_tok_stride = q.data_ptr(), q.stride(1), q.stride(2)
+        a.k_new, a.kn_head_stride, a.kn_tok_stride = k.data_ptr(), k.stride(1), k.stride(2)
+        a.v_new, a.vn_head_stride, a.vn_tok_stride = v.data_ptr(), v.stride(1), v.stride(2)
+        a.arena, a.tiles = self.arena.data_ptr(), self.tiles.data_ptr()
+        a.n_tiles, a.past = self._tiles_before(past), past
+        a.layer, a.layers, a.heads, a.q_heads, a.nq = layer, self.layers, self.heads, q.shape[1], nq
+        if segments:
+            if len(segments) + 1 > _lib.DKV_MAX_CHUNK_SEGS + 1:
+                raise ValueError(f'at most {_lib.DKV_MAX_CHUNK_SEGS} chunk segments')
+            a.n_segs = len(segments) - 1
+            for i, b in enumerate(segments):
+                a.seg_bounds[i] = b
+        a.scale = self.dim ** -0.5
+        a.out = out.data_ptr()
+        a.out_tok_stride, a.out_head_stride = out.stride(1), out.stride(2)
+        a.out_dtype = 1 if out.dtype == torch.float32 else 0
+        a.path, a.splits = path, splits
+        return a
+
+    def _workspace_for(self, nbytes):
+        if self._workspace is None or self._workspace.numel() < nbytes or self._workspace.device != self.device:
+            self._workspace = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=self.device)
+        return self._workspace
+
+    def attend(self, q, k, v, layer, past, out_dtype=None, segments=None, path=0, splits=0):
+        """Causal attention of q over history [0, past) plus the native chunk (src/gpu_cache.py:96-104).
+
+        `segments` (optional) lists chunk boundaries [0, b1, ..., nq] for a block-diagonal batch of
+        independent continuations that share the history, e.g. QA candidates.
+        """
+        n = q.shape[-2]
+        if q.dim() != 4 or q.shape[0] != 1 or q.shape[-1] != self.dim or q.shape[1] % self.heads:
+            raise ValueError('attend expects q [1, q_heads, n, 64] with q_heads a multiple of heads')
+        if k.shape != (1, self.heads, n, self.dim) or v.shape != k.shape:
+            raise ValueError(f'attend expects the chunk k, v of shape [1, {self.heads}, {n}, {self.dim}]')
+        if past + n > self.capacity or past > self.seen[layer]:
+            raise ValueError('attend: history longer than the cache holds')
+        if q.device.type != 'cuda' or k.device != q.device or v.device != q.device:
+            raise ValueError('attend requires CUDA tensors on one device')
+        q, k, v = self._kv_view(q), self._kv_view(k), self._kv_view(v)
+        out = torch.empty((1, n, q.shape[1], self.dim), dtype=out_dtype or q.dtype, device=q.device)
+        a = self.attend_args(q, k, v, layer, past, out, segments, path, splits)
+        lib = _lib.load()
+        need = lib.dkv_attend_workspace_bytes(ctypes.byref(a))
+        if need:
+            ws = self._workspace_for(need)
+            a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+        _lib.check(lib.dkv_attend(ctypes.byref(a), _lib.stream_handle(self.device)), 'dkv_attend')
+        return out
+
+    def materialize(self, layer, out_dtype=None):
+        """Dequantized history of one layer: (k, v), each [1, H, seen, 64] (src/gpu_cache.py:106-112)."""
+        n = self.seen[layer]
+        out = torch.empty((2, self.heads, n, self.dim), dtype=out_dtype or self.dtype, device=self.device)
+        if n:
+            lib = _lib.load()
+            _lib.check(lib.dkv_reconstruct(self.arena.data_ptr(), self.tiles.data_ptr(), self._tiles_before(n), n,
+                                           layer, self.layers, self.heads, out.data_ptr(),
+                                           1 if out.dtype == torch.float32 else 0,
+                                           _lib.stream_handle(self.device)), 'dkv_reconstruct')
+        return out[0:1], out[1:2]
+
+    def update(self, key_states, value_states, layer_idx, cache_kwargs=None):
+        """HF Cache.update compatibility path (src/gpu_cache.py:114-119)."""
+        self.append(key_states, value_states, layer_idx)
+        k, v = self.materialize(layer_idx)
+        k[:, :, -key_states.shape[-2]:].copy_(key_states)
+        v[:, :, -value_states.shape[-2]:].copy_(value_states)
+        return k, v
+
+    def fork(self):
+        """Branch that shares the arena and tile table (src/gpu_cache.py:121-132).
+
+        Branches write only past the base's used bytes and tiles; branches of one base overwrite
+        the same region, so they must run one after another on one stream.
+        """
+        other = object.__new__(GPUCache)
+        other.__dict__ = self.__dict__.copy()
+        other.seen = self.seen.copy()
+        other.cursors = self.cursors.copy()
+        other.plan = self.plan.copy()
+        other.segments = self.segments.copy()
+        other.tile_starts = self.tile_starts.copy()
+        other.host_counts = self.host_counts.copy()
+        other._workspace = None
+        other.pending_bits = 16
+        return other
+
+    def accounting(self):
+        """Used vs. allocated bytes with the reference's keys (src/gpu_cache.py:134-149)."""
+        allocated = self.arena.numel() + self.tiles.numel()
+        used = {4: 0, 8: 0, 16: 0}
+        n = self.seen[0]
+        for start, end, bits, _ in self.plan:
+            used[bits] += max(0, min(n, end) - start)
+        payload = self.layers * 2 * self.heads * self.dim * sum(used[b] * b / 8 for b in used)
+        scales = self.layers * 2 * self.heads * 8 * (used[4] + used[8])
+        mapping = 16 * self._tiles_before(n)
+        return dict(gpu_cache_used_bytes=int(payload + scales + mapping),
+                    gpu_cache_allocated_bytes=allocated, cpu_cache_payload_bytes=0,
+                    payload_bytes=int(payload), quantization_metadata_bytes=int(scales),
+                    token_mapping_bytes=mapping, logical_index_capacity=self.capacity,
+                    precision_pool_capacities=self.caps,
+                    used_tokens=n, precision_token_counts=used,
+                    arena_used_bytes=self.arena_used)
+
+
+class PackBatch:
+    """A device job table for dkv_pack_batch plus the cache it writes; run() relaunches it."""
+
+    def __init__(self, cache, jobs, max_n, keep=()):
+        self.cache, self.max_n, self.n_jobs, self._keep = cache, max_n, len(jobs), keep
+        table = (_lib.PackJob * len(jobs))(*jobs)
+        raw = torch.frombuffer(bytearray(bytes(table)), dtype=torch.uint8)
+        self.table = raw.to(cache.device)
+        self.arena, self.arena_bytes, self.tiles = cache.arena, cache.arena_bytes, cache.tiles
+
+    def run(self):
+        lib = _lib.load()
+        _lib.check(lib.dkv_pack_batch(self.table.data_ptr(), self.n_jobs, self.max_n, self.arena.data_ptr(),
+                                      self.arena_bytes, self.tiles.data_ptr(), self.cache.layers,
+                                      self.cache.heads, _lib.stream_handle(self.cache.device)), 'dkv_pack_batch')
+
+
+def install_packed_attention(model):
+    """Routes LlamaAttention through the packed cache when given a GPUCache (src/gpu_cache.py:151-183).
+
+    All other caches keep the upstream forward. Accepts both the `past_key_value` keyword of
+    transformers 4.x and the `past_key_values` keyword of 5.x.
+    """
+    from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
+
+    def forward(module, hidden_states, position_embeddings=None, attention_mask=None, past_key_value=None,
+                cache_position=None, **kwargs):
+        cache = past_key_value if past_key_value is not None else kwargs.get('past_key_values')
+        fused = isinstance(cache, GPUCache) and cache.backend == 'fused'
+        fast_gqa = getattr(cache, 'fast_gqa', False)
+        if not fused and not fast_gqa:
+            if past_key_value is not None:
+                kwargs['past_key_value'] = past_key_value
+            return module._original_forward(hidden_states=hidden_states, position_embeddings=position_embeddings,
+                                            attention_mask=attention_mask, cache_position=cache_position, **kwargs)
+        if kwargs.get('output_attentions', False):
+            raise ValueError('Fused packed attention does not expose attention matrices')
+        shape = hidden_states.shape[:-1]
+        if fused and hasattr(module, '_qkv_weight'):
+            q, k, v = F.linear(hidden_states, module._qkv_weight).split(module._qkv_sizes, dim=-1)
+        else:
+            q, k, v = module.q_proj(hidden_states), module.k_proj(hidden_states), module.v_proj(hidden_states)
+        q = q.view(*shape, -1, module.head_dim).transpose(1, 2)
+        k = k.view(*shape, -1, module.head_dim).transpose(1, 2)
+        v = v.view(*shape, -1, module.head_dim).transpose(1, 2)
+        q, k = apply_rotary_pos_emb(q, k, *position_embeddings)
+        if fused:
+            past = cache.append(k, v, module.layer_idx)
+            output = cache.attend(q, k, v, module.layer_idx, past)
+        else:
+            k, v = cache.update(k, v, module.layer_idx, {'cache_position': cache_position})
+            mask = None if attention_mask is None else attention_mask[:, :, :, :k.shape[-2]]
+            output = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, dropout_p=0,
+                                                    is_causal=mask is None and q.shape[-2] > 1,
+                                                    scale=module.scaling, enable_gqa=True).transpose(1, 2)
+        return module.o_proj(output.reshape(*shape, -1).contiguous()), None
+
+    for module in model.modules():
+        if module.__class__.__name__ == 'LlamaAttention' and not hasattr(module, '_original_forward'):
+            module._original_forward = module.forward
+            module.forward = types.MethodType(forward, module)

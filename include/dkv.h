@@ -1,0 +1,144 @@
+/*
+ * dkv.h - C ABI of the MI355X packed mixed-precision KV-cache library (libdkv.so).
+ *
+ * Plain pointers, sizes and a hipStream_t passed as void*. No torch types cross
+ * this boundary. Every entry point returns 0 on success, DKV_EINVAL for a
+ * contract violation (the message is available from dkv_last_error()) or a
+ * positive hipError_t value for a runtime failure. No entry point synchronizes
+ * the stream it is given.
+ *
+ * Storage format (shared by every entry point):
+ *   - A cache owns one byte arena. A segment is one append at one bit width
+ *     (4, 8 or 16). It is cut into tiles of up to 64 tokens.
+ *   - Tile i of a segment starts at seg_offset + i * dkv_slab_bytes(64, bits).
+ *     Inside a tile, the sub-block of (layer, kv, head), with kv 0 = K and 1 = V,
+ *     starts at ((layer*2 + kv)*heads + head) * dkv_subblock_bytes(rows, bits).
+ *   - A sub-block holds `rows` payload rows of 64 elements, then (for 4/8 bit)
+ *     `rows` pairs of fp32 (offset a, scale s). 4-bit rows are 32 bytes, with the
+ *     low nibble holding the even element. 8-bit rows are 64 bytes. 16-bit rows
+ *     are the 128 input bytes unchanged. This is the byte format of the
+ *     reference's quantizer and GPU pools (src/kv_quantization.py:57-73,
+ *     src/gpu_kernels.py:24-46).
+ */
+#ifndef DKV_H
+#define DKV_H
+
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DKV_ABI_VERSION 1
+#define DKV_HEAD_DIM 64
+#define DKV_TILE_TOKENS 64
+#define DKV_MAX_CHUNK_SEGS 16
+#define DKV_EINVAL (-1)
+
+/* One 64-token tile of the arena. The cache keeps these in token order in a
+ * device array; the pack entry points write them, the attention and
+ * reconstruct entry points read them. */
+typedef struct dkv_tile {
+  int64_t offset;      /* byte offset of the tile in the arena */
+  int32_t token_start; /* logical index of the tile's first token */
+  uint16_t rows;       /* rows the tile holds (1..64) */
+  uint8_t bits;        /* 4, 8 or 16 */
+  uint8_t reserved;
+} dkv_tile;
+
+/* One append of n tokens of one layer into a segment. k and v are bf16 views
+ * [heads, n, 64] with element strides per head and per token and a contiguous
+ * last dimension (V may be a transposed view, as in the reference tests). */
+typedef struct dkv_pack_job {
+  const void* k;
+  const void* v;
+  int64_t k_head_stride, k_tok_stride;
+  int64_t v_head_stride, v_tok_stride;
+  int64_t seg_offset;      /* byte offset of the segment in the arena */
+  int32_t seg_rows;        /* tokens the segment can hold */
+  int32_t seg_token_start; /* logical index of the segment's first token */
+  int32_t row0;            /* first segment row written by this job */
+  int32_t n;               /* tokens appended by this job */
+  int32_t layer;
+  int32_t bits;            /* 4, 8 or 16 */
+  int32_t tile_index0;     /* table index of the segment's first tile */
+  int32_t write_tiles;     /* nonzero: also write the segment's tile descriptors */
+} dkv_pack_job;
+
+/* Causal attention of a query chunk over the packed history plus the chunk's
+ * own native K/V. Query row m of chunk segment c sees every history token
+ * (token < past) and chunk tokens j with seg_bounds[c] <= j <= m. One segment
+ * covering [0, nq) is the ordinary bottom-right causal mask. */
+typedef struct dkv_attn_args {
+  const void* q;     /* bf16 [q_heads, nq, 64] */
+  int64_t q_head_stride, q_tok_stride;
+  const void* k_new; /* bf16 [heads, nq, 64] */
+  int64_t kn_head_stride, kn_tok_stride;
+  const void* v_new; /* bf16 [heads, nq, 64] */
+  int64_t vn_head_stride, vn_tok_stride;
+  const void* arena;
+  const dkv_tile* tiles; /* device array; tiles with token_start < past are read */
+  int32_t n_tiles;       /* number of tiles covering [0, past) */
+  int32_t past;          /* history tokens */
+  int32_t layer, layers, heads, q_heads, nq;
+  int32_t n_segs;        /* 0 or 1: one causal segment */
+  int32_t seg_bounds[DKV_MAX_CHUNK_SEGS + 1];
+  float scale;           /* softmax scale, 1/8 for head_dim 64 */
+  void* out;             /* [nq, q_heads, 64] with the strides below */
+  int64_t out_tok_stride, out_head_stride;
+  int32_t out_dtype;     /* 0 = bf16, 1 = fp32 */
+  int32_t path;          /* 0 = auto, 1 = vector, 2 = MFMA */
+  int32_t splits;        /* 0 = auto; history split count per KV head */
+  int32_t reserved;
+  void* workspace;       /* device scratch of dkv_attend_workspace_bytes() */
+  int64_t workspace_bytes;
+} dkv_attn_args;
+
+/* Library version: DKV_ABI_VERSION. */
+int dkv_version(void);
+
+/* Message of the last DKV_EINVAL on the calling thread ("" if none). */
+const char* dkv_last_error(void);
+
+/* Bytes of one (layer, kv, head) sub-block of a tile of `rows` rows. */
+int64_t dkv_subblock_bytes(int32_t rows, int32_t bits);
+
+/* Bytes of a whole tile of `rows` rows: layers * 2 * heads sub-blocks. */
+int64_t dkv_slab_bytes(int32_t rows, int32_t bits, int32_t layers, int32_t heads);
+
+/* Pack one append into the arena. Replaces the reference's per-layer
+ * pack_rows launch (src/gpu_cache.py:89-92, src/gpu_kernels.py:11-46). The
+ * bytes, offsets and scales equal src/kv_quantization.py:41-77 bit for bit. */
+int dkv_pack(const dkv_pack_job* job, void* arena, int64_t arena_bytes,
+             dkv_tile* tiles, int32_t layers, int32_t heads, void* stream);
+
+/* Pack n_jobs appends in one launch. `jobs` is a DEVICE array. max_n bounds
+ * every job's n. There is no reference counterpart for batching: it is the
+ * whole-volume form of dkv_pack used when many (layer, frame) tiles are ready
+ * at once, e.g. a prefill of several frames. */
+int dkv_pack_batch(const dkv_pack_job* jobs, int32_t n_jobs, int32_t max_n,
+                   void* arena, int64_t arena_bytes, dkv_tile* tiles,
+                   int32_t layers, int32_t heads, void* stream);
+
+/* Dequantize tokens [0, n_tokens) of one layer into out[2, heads, n_tokens, 64]
+ * (bf16 or fp32 by out_dtype), as q*s + a in fp32 (src/kv_quantization.py:90-92).
+ * Replaces GPUCache.materialize's reconstruct launch (src/gpu_cache.py:106-112,
+ * src/gpu_kernels.py:107-119). */
+int dkv_reconstruct(const void* arena, const dkv_tile* tiles, int32_t n_tiles,
+                    int32_t n_tokens, int32_t layer, int32_t layers, int32_t heads,
+                    void* out, int32_t out_dtype, void* stream);
+
+/* Workspace bytes dkv_attend needs for these arguments. */
+int64_t dkv_attend_workspace_bytes(const dkv_attn_args* args);
+
+/* Fused packed-history causal GQA attention. Replaces GPUCache.attend's
+ * packed_attention launch (src/gpu_cache.py:96-104, src/gpu_kernels.py:71-105).
+ * Output rows are written to out + m*out_tok_stride + qh*out_head_stride
+ * (elements), the reference's [1, nq, q_heads, 64] layout when contiguous. */
+int dkv_attend(const dkv_attn_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DKV_H */

@@ -1,0 +1,150 @@
+"""The C ABI on the CPU: the library loads, exports what include/dkv.h declares, its struct
+layouts match the ctypes mirror, and invalid arguments fail before any device work."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from conftest import REPO
+from dkv import _lib
+from dkv.gpu_cache import segment_bytes, slab_bytes, subblock_bytes
+
+HEADER = os.path.join(REPO, 'include', 'dkv.h')
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r'^\s*(?:int|int64_t|const char\*)\s+(dkv_\w+)\s*\(', text, re.M)))
+
+
+def test_every_declared_symbol_is_exported():
+    lib = _lib.load()
+    names = declared_functions()
+    assert len(names) >= 9
+    for name in names:
+        assert hasattr(lib, name), name
+    assert {n for n, _, _ in _lib.SIGNATURES} == set(names)
+    assert lib.dkv_version() == 1
+
+
+STRUCT_PROBE = r'''
+#include <stdio.h>
+#include <stddef.h>
+#include "dkv.h"
+#define F(s, f) printf(#s " " #f " %zu\n", offsetof(s, f));
+int main(void) {
+  printf("dkv_tile size %zu\n", sizeof(dkv_tile));
+  printf("dkv_pack_job size %zu\n", sizeof(dkv_pack_job));
+  printf("dkv_attn_args size %zu\n", sizeof(dkv_attn_args));
+  %FIELDS%
+  return 0;
+}
+'''
+
+
+@pytest.mark.parametrize('cls,cname', [(_lib.Tile, 'dkv_tile'), (_lib.PackJob, 'dkv_pack_job'),
+                                       (_lib.AttnArgs, 'dkv_attn_args')])
+def test_struct_layout_matches_header(tmp_path, cls, cname):
+    fields = '\n'.join(f'F({cname}, {f})' for f, _ in cls._fields_)
+    src = tmp_path / 'probe.c'
+    src.write_text(STRUCT_PROBE.replace('%FIELDS%', fields))
+    exe = tmp_path / 'probe'
+    subprocess.run(['gcc', '-std=c11', '-I', os.path.dirname(HEADER), str(src), '-o', str(exe)], check=True)
+    lines = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split('\n')
+    sizes = {l.split()[0]: int(l.split()[2]) for l in lines if ' size ' in l}
+    assert sizes[cname] == ctypes.sizeof(cls)
+    for line in lines:
+        parts = line.split()
+        if len(parts) == 3 and parts[0] == cname and parts[1] != 'size':
+            assert getattr(cls, parts[1]).offset == int(parts[2]), parts[1]
+
+
+@pytest.mark.parametrize('bits', [4, 8, 16])
+def test_geometry_matches_python_mirror(bits):
+    for rows in range(1, 65):
+        assert _lib.subblock_bytes(rows, bits) == subblock_bytes(rows, bits)
+        assert _lib.slab_bytes(rows, bits, 32, 5) == slab_bytes(rows, bits, 32, 5)
+        assert subblock_bytes(rows, bits) % 16 == 0
+    assert subblock_bytes(64, bits) == 64 * {4: 40, 8: 72, 16: 128}[bits]
+    assert segment_bytes(150, bits, 2, 5) == 2 * slab_bytes(64, bits, 2, 5) + slab_bytes(22, bits, 2, 5)
+
+
+def job(**kw):
+    base = dict(k=16, v=16, k_head_stride=64, k_tok_stride=64 * 5, v_head_stride=64, v_tok_stride=64,
+                seg_offset=0, seg_rows=64, seg_token_start=0, row0=0, n=8, layer=0, bits=4,
+                tile_index0=0, write_tiles=0)
+    base.update(kw)
+    return _lib.PackJob(**base)
+
+
+@pytest.mark.parametrize('kw,msg', [
+    (dict(bits=5), 'bits'),
+    (dict(row0=60), 'outside a segment'),
+    (dict(layer=3), 'layer'),
+    (dict(seg_offset=8), 'misaligned'),
+    (dict(k=18), 'aligned'),
+    (dict(v_tok_stride=63), 'aligned'),
+])
+def test_pack_rejects_bad_jobs_without_touching_the_device(kw, msg):
+    lib = _lib.load()
+    j = job(**kw)
+    rc = lib.dkv_pack(ctypes.byref(j), ctypes.c_void_p(4096), 1 << 20, None, 2, 5, None)
+    assert rc == _lib.DKV_EINVAL
+    assert msg in lib.dkv_last_error().decode()
+    with pytest.raises(ValueError):
+        _lib.check(rc, 'dkv_pack')
+
+
+def test_pack_rejects_segment_past_arena_end():
+    lib = _lib.load()
+    j = job(seg_offset=1 << 20)
+    assert lib.dkv_pack(ctypes.byref(j), ctypes.c_void_p(4096), 1 << 20, None, 2, 5, None) == _lib.DKV_EINVAL
+
+
+def attn(**kw):
+    a = _lib.AttnArgs()
+    a.q = a.k_new = a.v_new = a.out = 4096
+    a.q_head_stride, a.q_tok_stride = 64 * 64, 64
+    a.kn_head_stride, a.kn_tok_stride = 64 * 64, 64
+    a.vn_head_stride, a.vn_tok_stride = 64 * 64, 64
+    a.layers, a.heads, a.q_heads, a.nq = 1, 5, 15, 64
+    a.out_tok_stride, a.out_head_stride = 15 * 64, 64
+    a.scale = 0.125
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize('kw,msg', [
+    (dict(q=0), 'null'),
+    (dict(q_heads=14), 'shape'),
+    (dict(n_segs=17), 'n_segs'),
+    (dict(out_dtype=2), 'out_dtype'),
+    (dict(q_tok_stride=60), 'aligned'),
+    (dict(n_tiles=3), 'null'),
+])
+def test_attend_rejects_bad_arguments(kw, msg):
+    lib = _lib.load()
+    a = attn(**kw)
+    assert lib.dkv_attend(ctypes.byref(a), None) == _lib.DKV_EINVAL
+    assert msg in lib.dkv_last_error().decode()
+
+
+def test_attend_rejects_bad_segments():
+    lib = _lib.load()
+    a = attn(n_segs=2)
+    a.seg_bounds[0], a.seg_bounds[1], a.seg_bounds[2] = 0, 70, 64
+    assert lib.dkv_attend(ctypes.byref(a), None) == _lib.DKV_EINVAL
+    a.seg_bounds[1] = 0
+    assert lib.dkv_attend(ctypes.byref(a), None) == _lib.DKV_EINVAL
+
+
+def test_attend_demands_workspace_when_split():
+    lib = _lib.load()
+    a = attn(past=4096, n_tiles=64, arena=4096, tiles=4096)
+    need = lib.dkv_attend_workspace_bytes(ctypes.byref(a))
+    assert need > 0
+    assert lib.dkv_attend(ctypes.byref(a), None) == _lib.DKV_EINVAL
+    assert 'workspace' in lib.dkv_last_error().decode()

@@ -1,0 +1,195 @@
+"""Attention parity on the GPU against the CPU oracle.
+
+Tolerances:
+  fp32 output vs the fp64 dequantize-then-SDPA oracle: max-abs <= 1e-3.
+  bf16 output vs the same oracle: |out - oracle| <= 1e-3 + 2^-8 |oracle| (the bf16 store rounds
+    to nearest, which costs at most half an ulp = 2^-8 relative).
+  bf16 output vs the reference kernel's bf16 semantics on the reference's own test distribution
+    (unit-normal values): max-abs <= 2e-2.
+  The reference's own scenarios keep their tolerances (atol .035, rtol .015; max-abs < .035).
+"""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from conftest import announce
+from dkv.gpu_cache import GPUCache
+from dkv.workloads import candidate_case, frame_chunk_case
+from oracle.attention import attention, dequant_rows, reference_semantics
+from oracle.kv_quantization import pack_rows
+
+pytestmark = pytest.mark.gpu
+
+
+def build(case, cuda, layers=1, plan_mode=False):
+    """Cache with the case's history appended tile by tile at layer 0; returns (cache, deq K, deq V)."""
+    H, past = case['k_hist'].shape[:2]
+    tiles = [(b, min(64, past - 64 * i)) for i, b in enumerate(case['bits'])]
+    nq = case['q'].shape[1]
+    c = GPUCache(tiles + [(16, nq)] if plan_mode else None, layers=layers, heads=H,
+                 max_tokens=past + nq + 64)
+    dk, dv = [], []
+    t0 = 0
+    for b, n in tiles:
+        k = case['k_hist'][:, t0:t0 + n]
+        v = case['v_hist'][:, t0:t0 + n]
+        c.select(b)
+        c.append(k[None].to(cuda), v[None].to(cuda), 0)
+        for src, dst in ((k, dk), (v, dv)):
+            dst.append(dequant_rows(*pack_rows(src, b), b))
+        t0 += n
+    return c, torch.cat(dk, 1), torch.cat(dv, 1)
+
+
+def oracle_out(case, dk, dv, segments=None):
+    k = torch.cat((dk, case['k_new'].float()), 1)
+    v = torch.cat((dv, case['v_new'].float()), 1)
+    return attention(case['q'], k, v, dk.shape[1], segments=segments)
+
+
+def run(c, case, cuda, out_dtype, segments=None, path=0, splits=0):
+    q, kn, vn = (case[x][None].to(cuda) for x in ('q', 'k_new', 'v_new'))
+    c.select(16)
+    past = c.append(kn, vn, 0)
+    out = c.attend(q, kn, vn, 0, past, out_dtype=out_dtype, segments=segments, path=path, splits=splits)
+    torch.cuda.synchronize()
+    return out[0].cpu().double()
+
+
+@pytest.mark.parametrize('past', [1024, 4096, 8128])
+def test_frame_chunk_fp32_within_1e3_of_fp64_oracle(cuda, past):
+    announce(f'attention frame chunk past={past} fp32 out')
+    case = frame_chunk_case(past, seed=past)
+    c, dk, dv = build(case, cuda)
+    got = run(c, case, cuda, torch.float32)
+    ref = oracle_out(case, dk, dv)
+    err = (got - ref).abs().max().item()
+    assert err <= 1e-3, err
+
+
+@pytest.mark.parametrize('past', [1024, 8128])
+def test_frame_chunk_bf16_faithfully_rounded(cuda, past):
+    announce(f'attention frame chunk past={past} bf16 out')
+    case = frame_chunk_case(past, seed=past + 1)
+    c, dk, dv = build(case, cuda)
+    got = run(c, case, cuda, torch.bfloat16)
+    ref = oracle_out(case, dk, dv)
+    assert torch.all((got - ref).abs() <= 1e-3 + ref.abs() * 2.0 ** -8)
+
+
+def test_bf16_within_2e2_of_reference_semantics_on_unit_normal_data(cuda):
+    announce('attention vs reference bf16 semantics, unit-normal data')
+    g = torch.Generator().manual_seed(21)
+    past, nq = 1024, 64
+    case = dict(k_hist=torch.randn(5, past, 64, generator=g).bfloat16(),
+                v_hist=torch.randn(5, past, 64, generator=g).bfloat16(),
+                q=torch.randn(15, nq, 64, generator=g).bfloat16(),
+                k_new=torch.randn(5, nq, 64, generator=g).bfloat16(),
+                v_new=torch.randn(5, nq, 64, generator=g).bfloat16(),
+                bits=[4, 8, 16, 4] * 4)
+    c, dk, dv = build(case, cuda)
+    got = run(c, case, cuda, torch.bfloat16)
+    k = torch.cat((dk, case['k_new'].float()), 1)
+    v = torch.cat((dv, case['v_new'].float()), 1)
+    ref = reference_semantics(case['q'], k, v, past).double()
+    assert (got - ref).abs().max().item() <= 2e-2
+
+
+def test_plan_mode_and_partial_tiles(cuda):
+    announce('attention plan mode, partial tiles')
+    case = frame_chunk_case(1000, seed=5, nq=37)
+    c, dk, dv = build(case, cuda, plan_mode=True)
+    got = run(c, case, cuda, torch.float32)
+    assert (got - oracle_out(case, dk, dv)).abs().max().item() <= 1e-3
+
+
+@pytest.mark.parametrize('nq', [1, 5, 16, 77, 130])
+def test_chunk_lengths(cuda, nq):
+    announce(f'attention nq={nq}')
+    case = frame_chunk_case(640, seed=nq, nq=nq)
+    c, dk, dv = build(case, cuda)
+    got = run(c, case, cuda, torch.float32)
+    assert (got - oracle_out(case, dk, dv)).abs().max().item() <= 1e-3
+
+
+@pytest.mark.parametrize('splits', [1, 3, 1000])
+def test_split_counts_agree(cuda, splits):
+    announce(f'attention splits={splits}')
+    case = frame_chunk_case(2048, seed=3)
+    c, dk, dv = build(case, cuda)
+    got = run(c, case, cuda, torch.float32, splits=splits)
+    assert (got - oracle_out(case, dk, dv)).abs().max().item() <= 1e-3
+
+
+@pytest.mark.parametrize('bits', [4, 8])
+def test_candidates_block_diagonal(cuda, bits):
+    announce(f'attention candidates bits={bits}')
+    case = candidate_case(bits, seed=2, past=1536)
+    c, dk, dv = build(case, cuda)
+    got = run(c, case, cuda, torch.float32, segments=case['segments'])
+    ref = oracle_out(case, dk, dv, segments=case['segments'])
+    assert (got - ref).abs().max().item() <= 1e-3
+
+
+def test_empty_history(cuda):
+    announce('attention past=0')
+    case = frame_chunk_case(0, seed=1, nq=70)
+    c = GPUCache(None, layers=1, heads=5, max_tokens=256)
+    got = run(c, case, cuda, torch.float32)
+    ref = oracle_out(case, case['k_hist'].float(), case['v_hist'].float())
+    assert (got - ref).abs().max().item() <= 1e-3
+
+
+# -- the reference's own GPU scenarios ---------------------------------------------------------
+@pytest.mark.parametrize('query_length', [1, 77])
+def test_mixed_attention_five_kv_heads_and_long_history(cuda, query_length):
+    # tests/test_gpu_backend.py:157-176
+    announce(f'reference scenario query_length={query_length}')
+    torch.manual_seed(97)
+    c = GPUCache(None, layers=1, heads=5, max_tokens=2048)
+    for bits, n in [(4, 501), (8, 498)]:
+        k = torch.randn(1, 5, n, 64, device=cuda, dtype=torch.bfloat16)
+        v = torch.randn(1, n, 5, 64, device=cuda, dtype=torch.bfloat16).transpose(1, 2)
+        c.select(bits)
+        c.append(k, v, 0)
+    hk, hv = c.materialize(0)
+    n = query_length
+    q = torch.randn(1, 15, n, 64, device=cuda, dtype=torch.bfloat16)
+    k = torch.randn(1, 5, n, 64, device=cuda, dtype=torch.bfloat16)
+    v = torch.randn(1, n, 5, 64, device=cuda, dtype=torch.bfloat16).transpose(1, 2)
+    c.select(16)
+    past = c.append(k, v, 0)
+    actual = c.attend(q, k, v, 0, past)
+    full_k = torch.cat((hk, k), 2).float().cpu().repeat_interleave(3, 1)
+    full_v = torch.cat((hv, v), 2).float().cpu().repeat_interleave(3, 1)
+    mask = torch.arange(past + n)[None, :] <= past + torch.arange(n)[:, None]
+    expected = F.scaled_dot_product_attention(q.float().cpu(), full_k, full_v, attn_mask=mask).transpose(1, 2)
+    assert torch.allclose(actual.float().cpu(), expected.bfloat16().float(), atol=.035, rtol=.015)
+
+
+def test_sequential_mixed_appends_script_scenario(cuda):
+    # scripts/test_gpu_backend.py:12-37: plan mode, 9 Q / 3 KV heads, compare with SDPA each step.
+    announce('reference script scenario')
+    torch.manual_seed(12)
+    for bits_list in [[16, 16, 16], [4, 8, 16], [8, 4, 8]]:
+        lengths = [15, 67, 23]
+        cache = GPUCache(list(zip(bits_list, lengths)), layers=1)
+        full_k = full_v = None
+        for bits, n in zip(bits_list, lengths):
+            q = torch.randn((1, 9, n, 64), device=cuda, dtype=torch.bfloat16)
+            k = torch.randn((1, 3, n, 64), device=cuda, dtype=torch.bfloat16)
+            v = torch.randn_like(k)
+            cache.select(bits)
+            past = cache.append(k, v, 0)
+            out = cache.attend(q, k, v, 0, past)
+            rk = torch.cat([full_k, k], 2) if past else k
+            rv = torch.cat([full_v, v], 2) if past else v
+            mask = torch.arange(rk.shape[-2], device=cuda)[None, :] <= past + torch.arange(n, device=cuda)[:, None]
+            ref = F.scaled_dot_product_attention(q.float().cpu(), rk.float().cpu().repeat_interleave(3, 1),
+                                                 rv.float().cpu().repeat_interleave(3, 1),
+                                                 attn_mask=mask.cpu()).transpose(1, 2)
+            diff = (out.float().cpu() - ref).abs().max().item()
+            assert diff < .035, (bits_list, n, diff)
+            full_k, full_v = cache.materialize(0)
+            if bits == 16:
+                assert torch.equal(full_k[:, :, -n:], k)

@@ -1,0 +1,97 @@
+"""Ports of the reference's GPU cache tests (tests/test_gpu_backend.py:13-54) plus fork/growth."""
+import pytest
+import torch
+
+from conftest import announce
+from dkv.gpu_cache import GPUCache
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize('bits', [4, 8, 16])
+def test_gpu_pack_independent_error_bound(cuda, bits):
+    announce(f'error bound bits={bits}')
+    torch.manual_seed(71)
+    k = torch.randn((1, 3, 19, 64), device=cuda, dtype=torch.bfloat16)
+    v = torch.randn((1, 19, 3, 64), device=cuda, dtype=torch.bfloat16).transpose(1, 2)
+    c = GPUCache([(bits, 19)], layers=1)
+    c.select(bits)
+    c.append(k, v, 0)
+    rk, rv = c.materialize(0)
+    for x, y in [(k, rk), (v, rv)]:
+        if bits == 16:
+            assert torch.equal(x, y)
+        else:
+            xf = x.float()
+            scale = (xf.amax(-1, keepdim=True) - xf.amin(-1, keepdim=True)) / ((1 << bits) - 1)
+            assert torch.all((xf - y.float()).abs() <= scale * .501 + .032)
+
+
+def test_gpu_branch_does_not_advance_video_cache(cuda):
+    announce('fork does not advance base')
+    c = GPUCache([(4, 20), (16, 10)], layers=1)
+    k = torch.randn(1, 3, 20, 64, device=cuda, dtype=torch.bfloat16)
+    c.select(4)
+    c.append(k, k, 0)
+    before = c.materialize(0)[0].clone()
+    branch = c.fork()
+    q = torch.randn(1, 3, 5, 64, device=cuda, dtype=torch.bfloat16)
+    branch.append(q, q, 0)
+    assert c.get_seq_length() == 20 and branch.get_seq_length() == 25
+    assert torch.equal(c.materialize(0)[0], before)
+
+
+def test_online_growth_and_mapping(cuda):
+    announce('online growth and mapping')
+    c = GPUCache(None, layers=1, max_tokens=512)
+    expected = []
+    for i, (bits, n) in enumerate([(4, 79), (8, 93), (4, 88), (16, 71)]):
+        x = torch.randn(1, 3, n, 64, device=cuda, dtype=torch.bfloat16)
+        c.select(bits, i)
+        c.append(x, x, 0)
+        expected.extend([bits] * n)
+    assert c.codes[:len(expected)].tolist() == expected
+    assert c.caps[4] >= 167 and c.caps[8] >= 93 and c.caps[16] >= 71
+    assert c.get_seq_length() == len(expected)
+    before = c.materialize(0)[0].clone()
+    branch = c.fork()
+    branch.select(16)
+    z = torch.randn(1, 3, 90, 64, device=cuda, dtype=torch.bfloat16)
+    old_caps = c.caps.copy()
+    branch.append(z, z, 0)
+    assert c.caps == old_caps
+    assert torch.equal(c.materialize(0)[0], before)
+
+
+def test_growth_keeps_history_and_forks_keep_old_arena(cuda):
+    announce('arena growth')
+    c = GPUCache(None, layers=2, heads=5, max_tokens=1024, arena_bytes=1 << 16)
+    xs = []
+    for i in range(6):
+        x = torch.randn(1, 5, 64, 64, device=cuda, dtype=torch.bfloat16)
+        c.select(16)
+        for layer in range(2):
+            c.append(x, x, layer)
+        xs.append(x)
+    assert c.arena_bytes > 1 << 16
+    k, _ = c.materialize(1)
+    assert torch.equal(k, torch.cat(xs, 2))
+
+
+def test_candidate_forks_sequentially_reuse_the_qa_region(cuda):
+    announce('sequential candidate forks')
+    torch.manual_seed(5)
+    c = GPUCache(None, layers=1, heads=5, max_tokens=1024)
+    h = torch.randn(1, 5, 256, 64, device=cuda, dtype=torch.bfloat16)
+    c.select(4)
+    c.append(h, h, 0)
+    outs = []
+    for _ in range(2):
+        for n in (9, 17):
+            b = c.fork()
+            q = torch.randn(1, 15, n, 64, device=cuda, dtype=torch.bfloat16)
+            k = torch.randn(1, 5, n, 64, device=cuda, dtype=torch.bfloat16)
+            past = b.append(k, k, 0)
+            outs.append((past, b.attend(q, k, k, 0, past).clone()))
+    assert all(p == 256 for p, _ in outs)
+    assert c.get_seq_length() == 256 and len(c.segments) == 1

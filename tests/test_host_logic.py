@@ -1,0 +1,77 @@
+"""GPUCache bookkeeping on the CPU (device='cpu' arenas; no kernel runs)."""
+import pytest
+import torch
+
+from dkv.gpu_cache import GPUCache, segment_bytes, worst_case_arena_bytes
+
+
+def test_rejects_bad_geometry_and_plans():
+    with pytest.raises(ValueError):
+        GPUCache(dim=128, device='cpu')
+    with pytest.raises(ValueError):
+        GPUCache([(5, 10)], device='cpu')
+    with pytest.raises(ValueError):
+        GPUCache([(4, -1)], device='cpu')
+
+
+def test_plan_layout_matches_reference_plan_tuples():
+    c = GPUCache([(16, 15), (4, 67), (8, 23), (4, 10)], layers=2, heads=3, device='cpu')
+    # (start, end, bits, row within width class) as src/gpu_cache.py:25-29 builds them
+    assert c.plan == [(0, 15, 16, 0), (15, 82, 4, 0), (82, 105, 8, 0), (105, 115, 4, 67)]
+    assert c.host_counts == {4: 77, 8: 23, 16: 15}
+    assert c.capacity == 115
+    assert c.tile_starts == [0, 15, 79, 82, 105]
+    offs = [s.offset for s in c.segments]
+    sizes = [segment_bytes(s.rows, s.bits, 2, 3) for s in c.segments]
+    assert offs == [sum(sizes[:i]) for i in range(4)]
+    assert c.arena_used == sum(sizes) == c.arena_bytes
+    assert c.codes.tolist() == [16] * 15 + [4] * 67 + [8] * 23 + [4] * 10
+    assert c.rows.tolist()[:16] == list(range(15)) + [0]
+    assert c.rows.tolist()[105:] == list(range(67, 77))
+
+
+def test_append_requires_a_device_tensor():
+    c = GPUCache(None, layers=1, device='cpu')
+    with pytest.raises(ValueError):
+        c.append(torch.zeros(1, 3, 4, 64), torch.zeros(1, 3, 4, 64), 0)
+    with pytest.raises(ValueError):
+        c.append(torch.zeros(2, 3, 4, 64), torch.zeros(2, 3, 4, 64), 0)
+
+
+def test_online_arena_holds_any_mix():
+    c = GPUCache(None, layers=4, heads=5, max_tokens=512, device='cpu')
+    assert c.arena_bytes == worst_case_arena_bytes(512, 4, 5)
+    # 512 one-token 16-bit segments, the costliest cut, still fit
+    assert 512 * segment_bytes(1, 16, 4, 5) <= c.arena_bytes
+    assert c.caps[16] >= 512 and c.caps[4] >= c.caps[8] >= c.caps[16]
+
+
+def test_fork_copies_host_state_and_shares_storage():
+    c = GPUCache([(4, 20), (16, 10)], layers=1, device='cpu')
+    b = c.fork()
+    assert b.arena is c.arena and b.tiles is c.tiles
+    assert b.seen is not c.seen and b.plan is not c.plan and b.segments is not c.segments
+    assert b.pending_bits == 16
+    b.seen[0] = 5
+    assert c.seen[0] == 0
+
+
+def test_reserve_grows_only_the_caller():
+    c = GPUCache(None, layers=1, heads=3, max_tokens=256, arena_bytes=4096, device='cpu')
+    b = c.fork()
+    old = c.arena
+    b.reserve(16, 200)
+    assert b.arena is not old and b.arena_bytes >= segment_bytes(200, 16, 1, 3)
+    assert c.arena is old and c.arena_bytes == 4096
+
+
+def test_accounting_reference_identities():
+    c = GPUCache([(4, 64), (8, 64), (16, 64)], layers=2, heads=5, device='cpu')
+    c.seen = [192, 192]
+    a = c.accounting()
+    assert a['payload_bytes'] == 2 * 2 * 5 * 64 * (64 * 4 // 8 + 64 * 8 // 8 + 64 * 16 // 8)
+    assert a['quantization_metadata_bytes'] == 2 * 2 * 5 * 8 * 128
+    assert a['gpu_cache_used_bytes'] == a['payload_bytes'] + a['quantization_metadata_bytes'] + a['token_mapping_bytes']
+    assert a['precision_token_counts'] == {4: 64, 8: 64, 16: 64}
+    assert a['gpu_cache_allocated_bytes'] >= a['arena_used_bytes']
+    assert a['used_tokens'] == 192 and a['token_mapping_bytes'] == 3 * 16

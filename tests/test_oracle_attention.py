@@ -1,0 +1,107 @@
+"""Pins oracle/attention.py on the CPU."""
+import math
+
+import pytest
+import torch
+
+from oracle.attention import attention, dequant_rows, reference_semantics, visible_mask
+from oracle.kv_quantization import pack, pack_rows, unpack
+
+
+def loop_attention(q, k, v, past, scale):
+    """Pure-Python triple loop: softmax(scale q.k) v, causal chunk, kv head = qh // G."""
+    hq, nq, d = q.shape
+    g = hq // k.shape[0]
+    out = [[[0.0] * d for _ in range(hq)] for _ in range(nq)]
+    for qh in range(hq):
+        kh = qh // g
+        for m in range(nq):
+            keys = range(past + m + 1)
+            s = [scale * sum(q[qh, m, i].item() * k[kh, t, i].item() for i in range(d)) for t in keys]
+            mx = max(s)
+            e = [math.exp(x - mx) for x in s]
+            z = sum(e)
+            for i in range(d):
+                out[m][qh][i] = sum(e[t] * v[kh, t, i].item() for t in keys) / z
+    return torch.tensor(out, dtype=torch.float64)
+
+
+def test_matches_python_loop():
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(4, 3, 8, generator=g)
+    k = torch.randn(2, 7, 8, generator=g)
+    v = torch.randn(2, 7, 8, generator=g)
+    got = attention(q, k, v, past=4, scale=0.3)
+    assert torch.allclose(got, loop_attention(q, k, v, 4, 0.3), atol=1e-12)
+
+
+def test_identical_keys_give_mean_of_visible_values():
+    g = torch.Generator().manual_seed(6)
+    q = torch.randn(3, 5, 64, generator=g)
+    k = torch.randn(1, 1, 64, generator=g).expand(1, 12, 64)
+    v = torch.randn(1, 12, 64, generator=g)
+    out = attention(q, k, v, past=7)
+    for m in range(5):
+        expect = v[0, :8 + m].double().mean(0)
+        assert torch.allclose(out[m], expect.expand(3, 64), atol=1e-12)
+
+
+def test_gqa_head_map_uses_qh_div_group():
+    q = torch.randn(15, 4, 64)
+    k = torch.randn(5, 10, 64)
+    v = torch.arange(5, dtype=torch.float32)[:, None, None].expand(5, 10, 64)
+    out = attention(q, k, v, past=6)
+    for qh in range(15):
+        assert torch.allclose(out[:, qh], torch.full((4, 64), float(qh // 3), dtype=torch.float64))
+
+
+def test_segments_equal_separate_calls():
+    g = torch.Generator().manual_seed(8)
+    past, lens = 20, [3, 5, 2]
+    nq = sum(lens)
+    q = torch.randn(6, nq, 64, generator=g)
+    k = torch.randn(2, past + nq, 64, generator=g)
+    v = torch.randn(2, past + nq, 64, generator=g)
+    bounds = [0, 3, 8, 10]
+    got = attention(q, k, v, past, segments=bounds)
+    for c in range(3):
+        lo, hi = bounds[c], bounds[c + 1]
+        kc = torch.cat((k[:, :past], k[:, past + lo:past + hi]), 1)
+        vc = torch.cat((v[:, :past], v[:, past + lo:past + hi]), 1)
+        alone = attention(q[:, lo:hi], kc, vc, past)
+        assert torch.allclose(got[lo:hi], alone, atol=1e-12)
+
+
+def test_visible_mask_shape_and_causality():
+    m = visible_mask(3, 4)
+    assert m.shape == (4, 7) and m[:, :3].all()
+    assert m[0, 3] and not m[0, 4] and m[3, 6]
+
+
+def test_dequant_rows_equals_unpack():
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(3, 10, 64, generator=g)
+    for bits in (4, 8):
+        payload, off, sc = pack_rows(x, bits)
+        ref = unpack(pack(x.view(1, 3, 10, 64), bits), torch.float32).view(3, 10, 64)
+        assert torch.equal(dequant_rows(payload, off, sc, bits), ref)
+
+
+@pytest.mark.parametrize('query_length', [1, 77])
+def test_reference_scenario_semantics_within_reference_tolerance(query_length):
+    # tests/test_gpu_backend.py:157-176: 4-bit 501 + 8-bit 498 history, 5 KV / 15 Q heads.
+    torch.manual_seed(97)
+    hist = []
+    for bits, n in [(4, 501), (8, 498)]:
+        x = torch.randn(2, 5, n, 64).bfloat16()
+        hist.append(torch.stack([unpack(pack(x[i:i + 1], bits), torch.float32)[0] for i in range(2)]))
+    hk = torch.cat([h[0] for h in hist], 1)
+    hv = torch.cat([h[1] for h in hist], 1)
+    n = query_length
+    q = torch.randn(15, n, 64).bfloat16()
+    kn, vn = torch.randn(5, n, 64).bfloat16(), torch.randn(5, n, 64).bfloat16()
+    k = torch.cat((hk, kn.float()), 1)
+    v = torch.cat((hv, vn.float()), 1)
+    exact = attention(q, k, v, past=hk.shape[1])
+    emulated = reference_semantics(q, k, v, past=hk.shape[1])
+    assert torch.allclose(emulated.double(), exact, atol=.035, rtol=.015)
