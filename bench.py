@@ -74,8 +74,9 @@ def bench_pack(steps, warmup):
     return dict(ms=ms, gbs=gbs, read_bytes=read, write_bytes=write, bits=vol['bits'])
 
 
-def attention_setup(past, rotate, bits, nq=64, segments=None, seed=0):
-    """`rotate` layers, each with its own copy of one seeded history; returns launchers."""
+def attention_setup(past, rotate, bits, nq=64, segments=None, seed=0, precision='bf16', path='auto', splits=0):
+    """`rotate` layers, each with its own copy of one seeded history, and one graph that runs
+    the attention of every layer once (distinct histories, so the reads come from HBM)."""
     import ctypes
     import torch
     from dkv import _lib
@@ -88,7 +89,7 @@ def attention_setup(past, rotate, bits, nq=64, segments=None, seed=0):
     q = outlier_values((Q_HEADS, nq, 64), g, 0).to(dev)[None]
     kn = outlier_values((HEADS, nq, 64), g, 0).to(dev)[None]
     vn = outlier_values((HEADS, nq, 64), g, 0).to(dev)[None]
-    cache = GPUCache(None, layers=rotate, heads=HEADS, max_tokens=past + nq)
+    cache = GPUCache(None, layers=rotate, heads=HEADS, max_tokens=past + nq, precision=precision)
     tiles = (past + TILE - 1) // TILE
     lengths = [min(TILE, past - TILE * i) for i in range(tiles)]
     cache.append_batch(hk[None].expand(rotate, -1, -1, -1).contiguous(),
@@ -98,24 +99,32 @@ def attention_setup(past, rotate, bits, nq=64, segments=None, seed=0):
         cache.append(kn, vn, layer)
     out = torch.empty((1, nq, Q_HEADS, 64), dtype=torch.bfloat16, device=dev)
     lib = _lib.load()
-    args = [cache.attend_args(q, kn, vn, layer, past, out, segments) for layer in range(rotate)]
+    args = [cache.attend_args(q, kn, vn, layer, past, out, segments, path=path, splits=splits)
+            for layer in range(rotate)]
     need = lib.dkv_attend_workspace_bytes(ctypes.byref(args[0]))
-    ws = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+    ws = torch.zeros(max(need, 16), dtype=torch.uint8, device=dev)
     for a in args:
         a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
-    stream = _lib.stream_handle(dev)
     refs = [ctypes.byref(a) for a in args]
-    state = {'i': 0}
 
-    def launch():
-        i = state['i']
-        rc = lib.dkv_attend(refs[i], stream)
-        if rc:
-            _lib.check(rc, 'dkv_attend')
-        state['i'] = (i + 1) % rotate
+    def launch_all():
+        stream = _lib.stream_handle(dev)
+        for r in refs:
+            rc = lib.dkv_attend(r, stream)
+            if rc:
+                _lib.check(rc, 'dkv_attend')
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        launch_all()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        launch_all()
+    torch.cuda.synchronize()
     hist_bytes = sum(HEADS * 2 * n * {4: 40, 8: 72, 16: 128}[b] for b, n in zip(bits, lengths))
     chunk_bytes = (Q_HEADS * nq * 64 * 2) * 2 + HEADS * nq * 64 * 2 * 2  # q + out, k_new + v_new
-    return launch, hist_bytes + chunk_bytes, dict(cache=cache, keep=(hk, hv, q, kn, vn, out, ws, args))
+    keep = dict(cache=cache, keep=(hk, hv, q, kn, vn, out, ws, args), graph=graph)
+    return graph.replay, hist_bytes + chunk_bytes, keep
 
 
 def attention_flops(past, lengths):
@@ -124,27 +133,27 @@ def attention_flops(past, lengths):
     return 4 * 64 * Q_HEADS * visible
 
 
-def bench_attention(past, steps, warmup, rotate):
+def bench_attention(past, steps, warmup, rotate, precision='bf16'):
     from dkv.workloads import bit_schedule
     bits = bit_schedule(past, (past + TILE - 1) // TILE)
-    launch, nbytes, keep = attention_setup(past, rotate, bits, seed=past)
-    ms = time_launches(launch, steps, warmup)
+    replay, nbytes, keep = attention_setup(past, rotate, bits, seed=past, precision=precision)
+    ms = time_launches(replay, max(1, steps // 10), max(1, warmup // 10)) / rotate
     flops = attention_flops(past, [64])
     del keep
     return dict(us_per_layer=ms * 1e3, gbs=nbytes / (ms * 1e-3) / 1e9, tflops=flops / (ms * 1e-3) / 1e12,
                 bytes=nbytes, flops=flops, mfma_frac=flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS)
 
 
-def bench_candidates(bits, steps, warmup, rotate):
+def bench_candidates(bits, steps, warmup, rotate, precision='bf16'):
     from dkv.workloads import candidate_lengths
     lengths = candidate_lengths(0, 4)
     bounds = [0]
     for n in lengths:
         bounds.append(bounds[-1] + n)
     past = 6144
-    launch, nbytes, keep = attention_setup(past, rotate, [bits] * (past // TILE), nq=bounds[-1], segments=bounds,
-                                           seed=bits)
-    ms = time_launches(launch, steps, warmup)
+    replay, nbytes, keep = attention_setup(past, rotate, [bits] * (past // TILE), nq=bounds[-1], segments=bounds,
+                                           seed=bits, precision=precision)
+    ms = time_launches(replay, max(1, steps // 10), max(1, warmup // 10)) / rotate
     flops = attention_flops(past, lengths)
     del keep
     return dict(us_per_batch=ms * 1e3, gbs=nbytes / (ms * 1e-3) / 1e9, tflops=flops / (ms * 1e-3) / 1e12,
@@ -213,17 +222,20 @@ def main():
         print(f"# pack: {res['pack']['ms'] * 1e3:.1f} us/launch, {res['pack']['gbs']:.0f} GB/s", flush=True)
     if args.only in ('attn', 'all'):
         res['attention'] = {}
-        for past in (1024, 4096, 8128):
-            r = bench_attention(past, args.steps, args.warmup, args.rotate)
-            res['attention'][f'past_{past}'] = r
-            print(f"# attn past={past}: {r['us_per_layer']:.2f} us/layer, {r['gbs']:.0f} GB/s, "
-                  f"{r['tflops']:.1f} TFLOP/s", flush=True)
+        for prec in ('bf16', 'fp32'):
+            for past in (1024, 4096, 8128):
+                r = bench_attention(past, args.steps, args.warmup, args.rotate, prec)
+                res['attention'][f'{prec}_past_{past}'] = r
+                print(f"# attn {prec} past={past}: {r['us_per_layer']:.2f} us/layer, {r['gbs']:.0f} GB/s, "
+                      f"{r['tflops']:.1f} TFLOP/s", flush=True)
     if args.only in ('cand', 'all'):
         res['candidates'] = {}
-        for bits in (4, 8):
-            r = bench_candidates(bits, args.steps, args.warmup, args.rotate)
-            res['candidates'][f'{bits}bit'] = r
-            print(f"# candidates {bits}-bit: {r['us_per_batch']:.2f} us, {r['gbs']:.0f} GB/s", flush=True)
+        for prec in ('bf16', 'fp32'):
+            for bits in (4, 8):
+                r = bench_candidates(bits, args.steps, args.warmup, args.rotate, prec)
+                res['candidates'][f'{prec}_{bits}bit'] = r
+                print(f"# candidates {prec} {bits}-bit: {r['us_per_batch']:.2f} us, {r['gbs']:.0f} GB/s, "
+                      f"{r['tflops']:.1f} TFLOP/s", flush=True)
     cpu = None if args.no_cpu else cpu_baselines()
     p = res.get('pack')
     line = dict(

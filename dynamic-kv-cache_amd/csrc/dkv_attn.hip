@@ -11,58 +11,11 @@
 // than one range per head, each workgroup writes unnormalized partial
 // (O, max, sum) and combine_kernel merges them with the usual log-sum-exp
 // rescaling. Softmax runs in base 2: x = score * scale * log2(e).
-#include "dkv_common.h"
-#include <math.h>
+#include "dkv_attn_common.h"
 
 namespace dkv {
 
-constexpr float LOG2E = 1.4426950408889634f;
 constexpr int ATT_THREADS = 256;
-
-struct Unit {
-  // history tile: src rows come from the arena; chunk piece: from k_new/v_new
-  bool chunk;
-  int first;  // first logical token (history) or chunk row (chunk)
-  int valid;  // rows present in this unit
-  int bits;
-  const uint8_t* ksub;
-  const uint8_t* vsub;
-  int rows;  // rows of the tile (sub-block stride basis)
-};
-
-__device__ __forceinline__ Unit get_unit(const dkv_attn_args& a, int u) {
-  Unit un;
-  if (u < a.n_tiles) {
-    const dkv_tile t = a.tiles[u];
-    un.chunk = false;
-    un.first = t.token_start;
-    un.valid = min((int)t.rows, a.past - t.token_start);
-    un.bits = t.bits;
-    un.rows = t.rows;
-    const int64_t sb = subblock_bytes(t.rows, t.bits);
-    const uint8_t* base = static_cast<const uint8_t*>(a.arena) + t.offset;
-    const int h = blockIdx.y;
-    un.ksub = base + ((int64_t)(a.layer * 2 + 0) * a.heads + h) * sb;
-    un.vsub = base + ((int64_t)(a.layer * 2 + 1) * a.heads + h) * sb;
-  } else {
-    const int c = u - a.n_tiles;
-    un.chunk = true;
-    un.first = c * TILE;
-    un.valid = min(TILE, a.nq - c * TILE);
-    un.bits = 16;
-    un.rows = TILE;
-    un.ksub = un.vsub = nullptr;
-  }
-  return un;
-}
-
-// Chunk segment of chunk row j (one segment when n_segs <= 1).
-__device__ __forceinline__ int chunk_seg_start(const dkv_attn_args& a, int j) {
-  int start = 0;
-  for (int s = 1; s < a.n_segs; ++s)
-    if (j >= a.seg_bounds[s]) start = a.seg_bounds[s];
-  return start;
-}
 
 // Dequantizes 16 consecutive elements [c*16, c*16+16) of row r of a unit into
 // fp32 (q*s + a with separately rounded multiply and add).
@@ -125,12 +78,17 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// ---------------------------------------------------------------------------
-// Vector path: fp32 everywhere. A wave owns VEC_RPW query rows; lane n scores
-// token n of the unit, lane d accumulates output column d.
-constexpr int VEC_RPW = 16;
-constexpr int VEC_ROWS = 4 * VEC_RPW;  // rows per workgroup
+__device__ __forceinline__ float round_bf16(float x) { return __uint_as_float(f32_to_bf16_rne(x) << 16); }
 
+// ---------------------------------------------------------------------------
+// Vector path, for query chunks too short for MFMA tiles (fewer than 16 rows
+// per KV head, e.g. one decode token). A wave owns VEC_RPW query rows; lane n
+// scores key n of the unit, lane d accumulates output column d. PREC 0 rounds
+// the dequantized K/V and p to bf16 where the reference kernel does
+// (src/gpu_kernels.py:93-94,102); PREC 1 stays in fp32 throughout.
+constexpr int VEC_RPW = VEC_ROWS / 4;
+
+template <int PREC>
 __global__ void __launch_bounds__(ATT_THREADS)
 attn_vec_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ part_o,
                 float2* __restrict__ part_ml) {
@@ -177,7 +135,7 @@ attn_vec_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ part
   }
 
   for (int u = u0; u < u1; ++u) {
-    const Unit un = get_unit(a, u);
+    const Unit un = get_unit(a, u, h);
     __syncthreads();  // previous unit's readers are done; Qs is staged
     {
       const int r = tid >> 2, c = tid & 3;
@@ -191,8 +149,8 @@ attn_vec_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ part
       }
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        Kt[r][c * 16 + i] = xk[i];
-        Vt[r][c * 16 + i] = xv[i];
+        Kt[r][c * 16 + i] = PREC ? xk[i] : round_bf16(xk[i]);
+        Vt[r][c * 16 + i] = PREC ? xv[i] : round_bf16(xv[i]);
       }
     }
     __syncthreads();
@@ -217,7 +175,7 @@ attn_vec_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ part
       const float p = vis ? exp2f(x - mnew) : 0.f;
       sm[i] = sm[i] * alpha + wave_sum(p);
       mx[i] = mnew;
-      Ps[w][lane] = p;
+      Ps[w][lane] = PREC ? p : round_bf16(p);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -250,7 +208,12 @@ attn_vec_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ part
   }
 }
 
-// Log-sum-exp merge of split partials: one thread per (row, column).
+// Log-sum-exp merge of split partials: one thread per (row, column). The
+// splits are read CB at a time with independent loads, so a row's partials
+// stream in a few round trips instead of one per split; the running
+// (max, sum, output) is rescaled as each batch arrives.
+constexpr int CB = 16;
+
 __global__ void __launch_bounds__(256)
 combine_kernel(dkv_attn_args a, int splits, const float* __restrict__ part_o,
                const float2* __restrict__ part_ml) {
@@ -261,34 +224,41 @@ combine_kernel(dkv_attn_args a, int splits, const float* __restrict__ part_o,
   const int r = idx >> 6, d = idx & 63;
   if (r >= R) return;
   const int64_t base = (int64_t)h * splits * R + r;
-  float M = -INFINITY;
-  for (int s = 0; s < splits; ++s) M = fmaxf(M, part_ml[base + (int64_t)s * R].x);
-  float L = 0.f, O = 0.f;
-  for (int s = 0; s < splits; ++s) {
-    const float2 ml = part_ml[base + (int64_t)s * R];
-    if (ml.x == -INFINITY) continue;
-    const float f = exp2f(ml.x - M);
-    L = fmaf(ml.y, f, L);
-    O = fmaf(part_o[(base + (int64_t)s * R) * D + d], f, O);
+  float M = -INFINITY, L = 0.f, O = 0.f;
+  for (int s0 = 0; s0 < splits; s0 += CB) {
+    float2 ml[CB];
+    float o[CB];
+#pragma unroll
+    for (int i = 0; i < CB; ++i) {
+      const int s = s0 + i;
+      ml[i] = s < splits ? part_ml[base + (int64_t)s * R] : make_float2(-INFINITY, 0.f);
+      o[i] = s < splits ? part_o[(base + (int64_t)s * R) * D + d] : 0.f;
+    }
+    float bm = M;
+#pragma unroll
+    for (int i = 0; i < CB; ++i) bm = fmaxf(bm, ml[i].x);
+    if (bm == -INFINITY) continue;
+    const float f0 = exp2f(M - bm);  // 0 when M is still -inf
+    L *= f0;
+    O *= f0;
+#pragma unroll
+    for (int i = 0; i < CB; ++i) {
+      if (ml[i].x == -INFINITY) continue;
+      const float f = exp2f(ml[i].x - bm);
+      L = fmaf(ml[i].y, f, L);
+      O = fmaf(o[i], f, O);
+    }
+    M = bm;
   }
-  const float o = O / L;
+  const float out = O / L;
   const int g = r / a.nq, m = r - g * a.nq;
   const int64_t off = (int64_t)m * a.out_tok_stride + (int64_t)(h * G + g) * a.out_head_stride + d;
-  if (a.out_dtype == 1) static_cast<float*>(a.out)[off] = o;
-  else static_cast<uint16_t*>(a.out)[off] = (uint16_t)f32_to_bf16_rne(o);
+  if (a.out_dtype == 1) static_cast<float*>(a.out)[off] = out;
+  else static_cast<uint16_t*>(a.out)[off] = (uint16_t)f32_to_bf16_rne(out);
 }
 
 // ---------------------------------------------------------------------------
 // Host side.
-
-struct Plan {
-  int path;        // 1 vector, 2 MFMA
-  int units;
-  int splits;
-  int row_groups;
-  int rows_per_group;
-  int64_t part_o_bytes, part_ml_bytes;
-};
 
 static int num_cus() {
   static int cus = 0;
@@ -326,6 +296,10 @@ static int check_args(const dkv_attn_args& a) {
         return DKV_EINVAL;
       }
   }
+  if (a.path < 0 || a.path > 2 || a.precision < 0 || a.precision > 1) {
+    set_error("dkv_attend: path must be 0 (auto), 1 (vector) or 2 (MFMA); precision 0 (bf16) or 1 (fp32)");
+    return DKV_EINVAL;
+  }
   if (a.out_dtype != 0 && a.out_dtype != 1) {
     set_error("dkv_attend: out_dtype must be 0 (bf16) or 1 (fp32)");
     return DKV_EINVAL;
@@ -343,15 +317,22 @@ static Plan make_plan(const dkv_attn_args& a) {
   Plan p;
   const int G = a.q_heads / a.heads;
   const int R = G * a.nq;
-  p.path = 1;
-  p.rows_per_group = VEC_ROWS;
+  p.path = a.path;
+  if (p.path == 0) p.path = R >= 16 ? 2 : 1;
+  p.precision = a.precision;
+  p.rows_per_group = p.path == 2 ? MFMA_ROWS : VEC_ROWS;
   p.row_groups = (R + p.rows_per_group - 1) / p.rows_per_group;
   p.units = a.n_tiles + (a.nq + TILE - 1) / TILE;
   int splits = a.splits;
   if (splits <= 0) {
-    const int target = 2 * num_cus();
     const int per = a.heads * p.row_groups;
-    splits = (target + per - 1) / per;
+    if (p.path == 2) {
+      // One 8-wave workgroup per CU, all resident at once: a grid one past
+      // the CU count would take a second round for a single workgroup.
+      splits = num_cus() / per;
+    } else {
+      splits = (2 * num_cus() + per - 1) / per;
+    }
   }
   if (splits > p.units) splits = p.units;
   if (splits < 1) splits = 1;
@@ -363,6 +344,15 @@ static Plan make_plan(const dkv_attn_args& a) {
     p.part_o_bytes = p.part_ml_bytes = 0;
   }
   return p;
+}
+
+int launch_attn_vec(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml, hipStream_t s) {
+  const dim3 grid(p.splits, a.heads, p.row_groups);
+  if (p.precision == 1)
+    hipLaunchKernelGGL(attn_vec_kernel<1>, grid, dim3(ATT_THREADS), 0, s, a, p.units, p.splits, part_o, part_ml);
+  else
+    hipLaunchKernelGGL(attn_vec_kernel<0>, grid, dim3(ATT_THREADS), 0, s, a, p.units, p.splits, part_o, part_ml);
+  return (int)hipGetLastError();
 }
 
 }  // namespace dkv
@@ -396,8 +386,8 @@ int dkv_attend(const dkv_attn_args* args, void* stream) {
   float* part_o = static_cast<float*>(a.workspace);
   float2* part_ml = reinterpret_cast<float2*>(static_cast<char*>(a.workspace) + p.part_o_bytes);
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(attn_vec_kernel, dim3(p.splits, a.heads, p.row_groups), dim3(ATT_THREADS), 0, s, a,
-                     p.units, p.splits, part_o, part_ml);
+  const int rc = p.path == 2 ? launch_attn_mfma(a, p, part_o, part_ml, s) : launch_attn_vec(a, p, part_o, part_ml, s);
+  if (rc) return rc;
   if (p.splits > 1) {
     const int R = (a.q_heads / a.heads) * a.nq;
     hipLaunchKernelGGL(combine_kernel, dim3((R * D + 255) / 256, a.heads), dim3(256), 0, s, a, p.splits,

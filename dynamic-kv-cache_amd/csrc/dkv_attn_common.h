@@ -1,0 +1,78 @@
+// Helpers shared by the vector and MFMA attention kernels: the unit walk over
+// history tiles and chunk pieces, chunk segment bounds, the execution plan and
+// the launchers each kernel file provides.
+#pragma once
+#include "dkv_common.h"
+#include <math.h>
+
+namespace dkv {
+
+constexpr float LOG2E = 1.4426950408889634f;
+
+// A unit is 64 keys of one KV head: a history tile of the arena, or a 64-row
+// piece of the chunk's own native K/V.
+struct Unit {
+  bool chunk;
+  int first;  // first logical token (history) or chunk row (chunk)
+  int valid;  // keys present in this unit
+  int bits;   // 4, 8 or 16 (chunk pieces are 16)
+  int rows;   // rows of the tile: the sub-block's row stride basis
+  const uint8_t* ksub;
+  const uint8_t* vsub;
+};
+
+__device__ __forceinline__ Unit get_unit(const dkv_attn_args& a, int u, int h) {
+  Unit un;
+  if (u < a.n_tiles) {
+    const dkv_tile t = a.tiles[u];
+    un.chunk = false;
+    un.first = t.token_start;
+    un.valid = min((int)t.rows, a.past - t.token_start);
+    un.bits = t.bits;
+    un.rows = t.rows;
+    const int64_t sb = subblock_bytes(t.rows, t.bits);
+    const uint8_t* base = static_cast<const uint8_t*>(a.arena) + t.offset;
+    un.ksub = base + ((int64_t)(a.layer * 2 + 0) * a.heads + h) * sb;
+    un.vsub = base + ((int64_t)(a.layer * 2 + 1) * a.heads + h) * sb;
+  } else {
+    const int c = u - a.n_tiles;
+    un.chunk = true;
+    un.first = c * TILE;
+    un.valid = min(TILE, a.nq - c * TILE);
+    un.bits = 16;
+    un.rows = TILE;
+    un.ksub = un.vsub = nullptr;
+  }
+  return un;
+}
+
+// First chunk row of the segment holding chunk row j (0 when n_segs <= 1).
+__device__ __forceinline__ int chunk_seg_start(const dkv_attn_args& a, int j) {
+  int start = 0;
+  for (int s = 1; s < a.n_segs; ++s)
+    if (j >= a.seg_bounds[s]) start = a.seg_bounds[s];
+  return start;
+}
+
+// Workspace of a split call: partial outputs [heads, splits, R, 64] fp32, then
+// partial (max, sum) [heads, splits, R] float2.
+struct Plan {
+  int path;       // 1 vector, 2 MFMA
+  int precision;  // 0 bf16 operands (reference rounding), 1 fp32-accurate
+  int units;
+  int splits;
+  int row_groups;
+  int rows_per_group;
+  int64_t part_o_bytes, part_ml_bytes;
+};
+
+// Launchers (return hipGetLastError()).
+int launch_attn_vec(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml,
+                    hipStream_t s);
+int launch_attn_mfma(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml,
+                     hipStream_t s);
+
+constexpr int VEC_ROWS = 64;    // query rows per vector-path workgroup
+constexpr int MFMA_ROWS = 192;  // query rows per MFMA-path workgroup (4 waves x 3 x 16)
+
+}  // namespace dkv

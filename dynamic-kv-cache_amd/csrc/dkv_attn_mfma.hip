@@ -1,0 +1,421 @@
+// MFMA path of the fused packed-history attention (gfx950,
+// v_mfma_f32_16x16x32_bf16), used when a KV head has at least 16 query rows
+// (a 64-token frame chunk times 3 GQA heads gives 192).
+//
+// Workgroup = 8 waves = one KV head, up to 192 query rows (every GQA head of
+// that KV head), one contiguous range of units (64-key history tiles, then
+// 64-row pieces of the chunk). The waves form two key groups: group c
+// (waves 4c..4c+3) handles keys [32c, 32c + 32) of every unit, so two waves
+// share each SIMD and one's softmax overlaps the other's MFMAs. Wave w of a
+// group owns 16-row query blocks w, w+4, w+8. The two groups keep separate
+// online-softmax states and merge through LDS after the last unit.
+//
+// Per unit:
+//   1. the raw K and V sub-blocks (codes + (offset, scale) pairs, or bf16 rows)
+//      are copied to LDS with one 16-byte load per thread each; the next
+//      unit's loads are issued before this unit's MFMA work;
+//   2. the 512 threads dequantize (q*s + a, fp32 multiply then add, as the
+//      reference unpack does) into a bf16 K tile [key][d] and a transposed
+//      bf16 V tile [d][key];
+//   3. each wave computes S^T = K Q^T for its blocks (keys on the MFMA M axis,
+//      queries on N), runs the online softmax per query column in registers,
+//      and accumulates O^T = V^T P^T with P^T taken straight from the S^T
+//      accumulators: key k of the group's 32 keys sits in S^T block j at row
+//      4g + i with k = 8g + 4j + i, so lane group g of blocks 0 and 1 holds
+//      keys 8g .. 8g+7, the eight k-slots the PV MFMA wants from that group.
+//
+// Splitting the history: with several splits per KV head each workgroup
+// writes unnormalized partials (O, running max, sum) to the workspace and
+// combine_kernel merges them. (Merging in the last-arriving workgroup instead
+// needs a device-scope fence per workgroup, which on gfx950 writes back and
+// invalidates the XCD's L2 and cost far more than the second launch.)
+//
+// Precision (template PREC):
+//   0  the reference kernel's rounding points (src/gpu_kernels.py:93-102):
+//      dequantized K/V and p are rounded to bf16, fp32 accumulation;
+//   1  fp32-accurate: K = K_hi + K_lo and V = V_hi + V_lo, p = p_hi + p_lo
+//      (bf16 pairs, 2^-17 relative), S = Q K_hi + Q K_lo and
+//      O = P_hi V_hi + P_hi V_lo + P_lo V_hi; the lo terms are skipped for
+//      bf16 units, where they are exactly zero.
+#include "dkv_attn_common.h"
+
+namespace dkv {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int MF_THREADS = 512;
+constexpr int KS = 72;       // LDS row stride, in bf16 elements, of the K and V^T tiles
+constexpr int RAWP = 9216;   // padded raw bytes of one sub-block (64 rows x 128 B + 16 B per 128 B)
+
+union Pack8 {
+  bf16x8 v;
+  uint4 u;
+};
+
+// Two fp32 -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), bf16x2));
+}
+__device__ __forceinline__ float bf16_lo_f(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi_f(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Raw sub-blocks sit in LDS with 16 bytes of padding after every 128 bytes,
+// which spreads the rows a dequantizing wave reads over all banks.
+__device__ __forceinline__ int padded(int off) { return off + ((off >> 7) << 4); }
+
+// 8 fp32 values of row r, columns [8*db, 8*db + 8), from a raw sub-block in LDS.
+__device__ __forceinline__ void dequant8(const uint8_t* raw, int bits, int rows, int r, int db, float* x) {
+  if (bits == 16) {
+    const uint4 w = *reinterpret_cast<const uint4*>(raw + padded(r * 128 + db * 16));
+    x[0] = bf16_lo_f(w.x); x[1] = bf16_hi_f(w.x);
+    x[2] = bf16_lo_f(w.y); x[3] = bf16_hi_f(w.y);
+    x[4] = bf16_lo_f(w.z); x[5] = bf16_hi_f(w.z);
+    x[6] = bf16_lo_f(w.w); x[7] = bf16_hi_f(w.w);
+    return;
+  }
+  const float2 as = *reinterpret_cast<const float2*>(raw + padded(rows * (int)row_bytes(bits) + 8 * r));
+  float q[8];
+  if (bits == 4) {
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(raw + padded(r * 32 + db * 4));
+    const uint32_t ev = w & 0x0f0f0f0fu, od = (w >> 4) & 0x0f0f0f0fu;  // even / odd elements
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      q[2 * i] = (float)((ev >> (8 * i)) & 255u);
+      q[2 * i + 1] = (float)((od >> (8 * i)) & 255u);
+    }
+  } else {
+    const uint2 w = *reinterpret_cast<const uint2*>(raw + padded(r * 64 + db * 8));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      q[i] = (float)((w.x >> (8 * i)) & 255u);
+      q[4 + i] = (float)((w.y >> (8 * i)) & 255u);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = __fadd_rn(__fmul_rn(q[i], as.y), as.x);
+}
+
+// One 16-byte piece of K (threads 0..511 -> pieces 0..511) and one of V.
+__device__ __forceinline__ void raw_load(const dkv_attn_args& a, const Unit& un, int h, uint4& wk, uint4& wv) {
+  const int p = threadIdx.x;
+  wk = wv = make_uint4(0, 0, 0, 0);
+  if (un.chunk) {
+    const int row = p >> 3, c = p & 7;
+    if (row < un.valid) {
+      const int64_t j = un.first + row;
+      wk = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.k_new) + h * a.kn_head_stride +
+                                           j * a.kn_tok_stride + c * 8);
+      wv = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.v_new) + h * a.vn_head_stride +
+                                           j * a.vn_tok_stride + c * 8);
+    }
+  } else if (p < (int)(subblock_bytes(un.rows, un.bits) >> 4)) {
+    wk = reinterpret_cast<const uint4*>(un.ksub)[p];
+    wv = reinterpret_cast<const uint4*>(un.vsub)[p];
+  }
+}
+
+// NBW = 16-row query blocks each wave computes (1..3). A wave whose first
+// block is past the last row skips the MFMA work (a scalar branch); other
+// waves compute all NBW blocks, those past the last row on zero queries, and
+// store only real rows.
+template <int PREC, int NBW>
+__global__ void __launch_bounds__(MF_THREADS)
+attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ part_o,
+                 float2* __restrict__ part_ml) {
+  __shared__ __attribute__((aligned(16))) uint8_t raw[2][RAWP];
+  __shared__ __attribute__((aligned(16))) uint16_t k_hi[64 * KS];
+  __shared__ __attribute__((aligned(16))) uint16_t v_hi[64 * KS];
+  __shared__ __attribute__((aligned(16))) uint16_t k_lo[PREC ? 64 * KS : 8];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lo[PREC ? 64 * KS : 8];
+  __shared__ __attribute__((aligned(16))) float mrg_o[MFMA_ROWS * D];
+  __shared__ float2 mrg_ml[MFMA_ROWS];
+
+  const int split = blockIdx.x, h = blockIdx.y, rg = blockIdx.z;
+  const int G = a.q_heads / a.heads;
+  const int R = G * a.nq;
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int kg = wave >> 2, w = wave & 3;  // key group, wave within the group
+  const int col = lane & 15, g = lane >> 4;
+  const int u0 = (int)((int64_t)units * split / splits);
+  const int u1 = (int)((int64_t)units * (split + 1) / splits);
+  const float xs = a.scale * LOG2E;
+  const bool wave_on = rg * MFMA_ROWS + w * 16 < R;  // wave-uniform
+
+  // Query operands and masking bounds of this lane's query column in each block.
+  bf16x8 qop[NBW][2];
+  int qlo[NBW], qhi[NBW];
+#pragma unroll
+  for (int nb = 0; nb < NBW; ++nb) {
+    const int r = rg * MFMA_ROWS + (w + 4 * nb) * 16 + col;
+    Pack8 q0, q1;
+    q0.u = q1.u = make_uint4(0, 0, 0, 0);
+    qlo[nb] = 0;
+    qhi[nb] = -1;
+    if (r < R) {
+      const int gq = r / a.nq, m = r - gq * a.nq;
+      const uint16_t* src = static_cast<const uint16_t*>(a.q) + (int64_t)(h * G + gq) * a.q_head_stride +
+                            (int64_t)m * a.q_tok_stride + 8 * g;
+      q0.u = *reinterpret_cast<const uint4*>(src);
+      q1.u = *reinterpret_cast<const uint4*>(src + 32);
+      qlo[nb] = chunk_seg_start(a, m);
+      qhi[nb] = m;
+    }
+    qop[nb][0] = q0.v;
+    qop[nb][1] = q1.v;
+  }
+
+  f32x4 acc_o[NBW][4];
+  float m_run[NBW], l_part[NBW];
+#pragma unroll
+  for (int nb = 0; nb < NBW; ++nb) {
+#pragma unroll
+    for (int db = 0; db < 4; ++db) acc_o[nb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    m_run[nb] = -INFINITY;
+    l_part[nb] = 0.f;
+  }
+
+  uint4 wk, wv;
+  if (u0 < u1) raw_load(a, get_unit(a, u0, h), h, wk, wv);
+
+  for (int u = u0; u < u1; ++u) {
+    const Unit un = get_unit(a, u, h);
+    *reinterpret_cast<uint4*>(raw[0] + padded(16 * t)) = wk;
+    *reinterpret_cast<uint4*>(raw[1] + padded(16 * t)) = wv;
+    __syncthreads();
+    // Dequantize into bf16 tiles: thread = (K or V, key pair kp, column block db).
+    {
+      const int kv = t >> 8, kp = (t & 255) >> 3, db = t & 7;
+      const int r0 = 2 * kp, r1 = r0 + 1;
+      float x0[8], x1[8];
+      if (r0 < un.valid) dequant8(raw[kv], un.bits, un.rows, r0, db, x0);
+      else
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x0[i] = 0.f;
+      if (r1 < un.valid) dequant8(raw[kv], un.bits, un.rows, r1, db, x1);
+      else
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x1[i] = 0.f;
+      if (kv == 0) {
+        uint4 h0, h1;
+        h0 = make_uint4(pk_bf16(x0[0], x0[1]), pk_bf16(x0[2], x0[3]), pk_bf16(x0[4], x0[5]), pk_bf16(x0[6], x0[7]));
+        h1 = make_uint4(pk_bf16(x1[0], x1[1]), pk_bf16(x1[2], x1[3]), pk_bf16(x1[4], x1[5]), pk_bf16(x1[6], x1[7]));
+        *reinterpret_cast<uint4*>(k_hi + r0 * KS + db * 8) = h0;
+        *reinterpret_cast<uint4*>(k_hi + r1 * KS + db * 8) = h1;
+        if (PREC) {
+          const uint32_t hw0[4] = {h0.x, h0.y, h0.z, h0.w}, hw1[4] = {h1.x, h1.y, h1.z, h1.w};
+          uint32_t l0[4], l1[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            l0[i] = pk_bf16(x0[2 * i] - bf16_lo_f(hw0[i]), x0[2 * i + 1] - bf16_hi_f(hw0[i]));
+            l1[i] = pk_bf16(x1[2 * i] - bf16_lo_f(hw1[i]), x1[2 * i + 1] - bf16_hi_f(hw1[i]));
+          }
+          *reinterpret_cast<uint4*>(k_lo + r0 * KS + db * 8) = make_uint4(l0[0], l0[1], l0[2], l0[3]);
+          *reinterpret_cast<uint4*>(k_lo + r1 * KS + db * 8) = make_uint4(l1[0], l1[1], l1[2], l1[3]);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t hv = pk_bf16(x0[i], x1[i]);
+          *reinterpret_cast<uint32_t*>(v_hi + (db * 8 + i) * KS + r0) = hv;
+          if (PREC)
+            *reinterpret_cast<uint32_t*>(v_lo + (db * 8 + i) * KS + r0) =
+                pk_bf16(x0[i] - bf16_lo_f(hv), x1[i] - bf16_hi_f(hv));
+        }
+      }
+    }
+    __syncthreads();
+    if (u + 1 < u1) raw_load(a, get_unit(a, u + 1, h), h, wk, wv);
+    if (!wave_on) continue;
+
+    const bool lo_on = PREC && un.bits != 16;
+    // S^T = K Q^T over this group's 32 keys: block j holds keys 32 kg + 8 g' + 4 j + i
+    // in its row 4 g' + i, so A-operand row `col` of block j is key
+    // 32 kg + 8 (col / 4) + 4 j + col % 4.
+    f32x4 sc[NBW][2];
+#pragma unroll
+    for (int nb = 0; nb < NBW; ++nb) sc[nb][0] = sc[nb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int pass = 0; pass < (PREC ? 2 : 1); ++pass) {
+      if (pass == 1 && !lo_on) break;
+      const uint16_t* kt = pass ? k_lo : k_hi;
+      Pack8 ka[2][2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int key = 32 * kg + 8 * (col >> 2) + 4 * j + (col & 3);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+          ka[j][ks].u = *reinterpret_cast<const uint4*>(kt + key * KS + 32 * ks + 8 * g);
+      }
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int nb = 0; nb < NBW; ++nb)
+            sc[nb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[j][ks].v, qop[nb][ks], sc[nb][j], 0, 0, 0);
+    }
+    // V^T operands: row d = 16 db + col, keys 32 kg + 8 g .. + 7.
+    Pack8 va[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+      va[db].u = *reinterpret_cast<const uint4*>(v_hi + (16 * db + col) * KS + 32 * kg + 8 * g);
+
+    // Online softmax per query column over the group's 32 keys (8 per lane).
+    Pack8 p_hi[NBW], p_lo[NBW];
+    const bool full = !un.chunk && un.valid == TILE;
+#pragma unroll
+    for (int nb = 0; nb < NBW; ++nb) {
+      float s[8];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[4 * j + i] = sc[nb][j][i];
+      if (!full) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int key = 32 * kg + 8 * g + e;  // e = 4 j + i
+          bool vis = key < un.valid;
+          if (un.chunk) {
+            const int jj = un.first + key;
+            vis = vis && jj >= qlo[nb] && jj <= qhi[nb];
+          }
+          s[e] = vis ? s[e] : -INFINITY;
+        }
+      }
+      float mt = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+      mt = fmaxf(mt, __shfl_xor(mt, 16));
+      mt = fmaxf(mt, __shfl_xor(mt, 32));
+      const float mnew = fmaxf(m_run[nb], mt * xs);
+      const bool none = mnew == -INFINITY;
+      const float alpha = none ? 1.f : __builtin_amdgcn_exp2f(m_run[nb] - mnew);
+      const float mref = none ? 0.f : mnew;
+      float p[8], psum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        p[e] = __builtin_amdgcn_exp2f(__fmaf_rn(s[e], xs, -mref));
+        psum += p[e];
+      }
+      l_part[nb] = __fmaf_rn(l_part[nb], alpha, psum);
+      m_run[nb] = mnew;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) acc_o[nb][db] *= alpha;
+      const uint32_t w0 = pk_bf16(p[0], p[1]), w1 = pk_bf16(p[2], p[3]);
+      const uint32_t w2 = pk_bf16(p[4], p[5]), w3 = pk_bf16(p[6], p[7]);
+      p_hi[nb].u = make_uint4(w0, w1, w2, w3);
+      if (PREC)
+        p_lo[nb].u = make_uint4(pk_bf16(p[0] - bf16_lo_f(w0), p[1] - bf16_hi_f(w0)),
+                                pk_bf16(p[2] - bf16_lo_f(w1), p[3] - bf16_hi_f(w1)),
+                                pk_bf16(p[4] - bf16_lo_f(w2), p[5] - bf16_hi_f(w2)),
+                                pk_bf16(p[6] - bf16_lo_f(w3), p[7] - bf16_hi_f(w3)));
+    }
+    // O^T += V^T P^T.
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int nb = 0; nb < NBW; ++nb)
+        acc_o[nb][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[db].v, p_hi[nb].v, acc_o[nb][db], 0, 0, 0);
+    if (PREC) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int nb = 0; nb < NBW; ++nb)
+          acc_o[nb][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[db].v, p_lo[nb].v, acc_o[nb][db], 0, 0, 0);
+      if (lo_on) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+          va[db].u = *reinterpret_cast<const uint4*>(v_lo + (16 * db + col) * KS + 32 * kg + 8 * g);
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int nb = 0; nb < NBW; ++nb)
+            acc_o[nb][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[db].v, p_hi[nb].v, acc_o[nb][db], 0, 0, 0);
+      }
+    }
+  }
+
+  // Merge the two key groups: group 1 parks (max, sum, O) in LDS, group 0
+  // folds it in. Lane (g, col) of block nb holds O^T rows d = 16 db + 4 g + i
+  // of local row (w + 4 nb) * 16 + col.
+  float lsum[NBW];
+#pragma unroll
+  for (int nb = 0; nb < NBW; ++nb) {
+    float l = l_part[nb];
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    lsum[nb] = l;
+  }
+  if (kg == 1 && wave_on) {
+#pragma unroll
+    for (int nb = 0; nb < NBW; ++nb) {
+      const int lr = (w + 4 * nb) * 16 + col;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+        *reinterpret_cast<f32x4*>(mrg_o + lr * D + 16 * db + 4 * g) = acc_o[nb][db];
+      if (g == 0) mrg_ml[lr] = make_float2(m_run[nb], lsum[nb]);
+    }
+  }
+  __syncthreads();
+  if (kg == 0 && wave_on) {
+#pragma unroll
+    for (int nb = 0; nb < NBW; ++nb) {
+      const int lr = (w + 4 * nb) * 16 + col;
+      const float2 o1 = mrg_ml[lr];
+      const float mm = fmaxf(m_run[nb], o1.x);
+      const float f0 = mm == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[nb] - mm);
+      const float f1 = mm == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(o1.x - mm);
+      const float l = lsum[nb] * f0 + o1.y * f1;
+      const int r = rg * MFMA_ROWS + lr;
+      f32x4 o[4];
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+        o[db] = acc_o[nb][db] * f0 + *reinterpret_cast<const f32x4*>(mrg_o + lr * D + 16 * db + 4 * g) * f1;
+      if (r >= R) continue;
+      if (splits == 1) {
+        const int gq = r / a.nq, m = r - gq * a.nq;
+        const float inv = 1.f / l;
+        const int64_t off = (int64_t)m * a.out_tok_stride + (int64_t)(h * G + gq) * a.out_head_stride + 4 * g;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          const f32x4 v = o[db] * inv;
+          if (a.out_dtype == 1)
+            *reinterpret_cast<float4*>(static_cast<float*>(a.out) + off + 16 * db) = make_float4(v[0], v[1], v[2], v[3]);
+          else
+            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + off + 16 * db) =
+                make_uint2(pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3]));
+        }
+      } else {
+        const int64_t base = ((int64_t)h * splits + split) * R + r;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+          *reinterpret_cast<float4*>(part_o + base * D + 16 * db + 4 * g) = make_float4(o[db][0], o[db][1], o[db][2], o[db][3]);
+        if (g == 0) part_ml[base] = make_float2(mm, l);
+      }
+    }
+  }
+}
+
+template <int PREC>
+static void launch_prec(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml, hipStream_t s) {
+  const dim3 grid(p.splits, a.heads, p.row_groups);
+  const int R = (a.q_heads / a.heads) * a.nq;
+  const int rows = R < MFMA_ROWS ? R : MFMA_ROWS;  // rows of the fullest row group
+  const int nbw = ((rows + 15) / 16 + 3) / 4;       // blocks of the busiest wave
+  if (nbw >= 3)
+    hipLaunchKernelGGL((attn_mfma_kernel<PREC, 3>), grid, dim3(MF_THREADS), 0, s, a, p.units, p.splits, part_o, part_ml);
+  else if (nbw == 2)
+    hipLaunchKernelGGL((attn_mfma_kernel<PREC, 2>), grid, dim3(MF_THREADS), 0, s, a, p.units, p.splits, part_o, part_ml);
+  else
+    hipLaunchKernelGGL((attn_mfma_kernel<PREC, 1>), grid, dim3(MF_THREADS), 0, s, a, p.units, p.splits, part_o, part_ml);
+}
+
+int launch_attn_mfma(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml, hipStream_t s) {
+  if (p.precision == 1) launch_prec<1>(a, p, part_o, part_ml, s);
+  else launch_prec<0>(a, p, part_o, part_ml, s);
+  return (int)hipGetLastError();
+}
+
+}  // namespace dkv

@@ -44,7 +44,7 @@ class AttnArgs(ctypes.Structure):
                 ('scale', ctypes.c_float),
                 ('out', ctypes.c_void_p), ('out_tok_stride', ctypes.c_int64), ('out_head_stride', ctypes.c_int64),
                 ('out_dtype', ctypes.c_int32), ('path', ctypes.c_int32), ('splits', ctypes.c_int32),
-                ('reserved', ctypes.c_int32),
+                ('precision', ctypes.c_int32),
                 ('workspace', ctypes.c_void_p), ('workspace_bytes', ctypes.c_int64)]
 
 

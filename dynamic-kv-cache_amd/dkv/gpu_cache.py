@@ -25,6 +25,10 @@ except Exception:  # transformers absent: a plain object base keeps the kernels 
 
 TILE = 64
 BITS = (4, 8, 16)
+# 'bf16': dequantized K/V and p rounded to bf16 before the dot products, as the reference kernel
+# does (src/gpu_kernels.py:93-94,102). 'fp32': fp32-accurate (split bf16 pairs on the MFMA path).
+PRECISIONS = {'bf16': 0, 'fp32': 1}
+PATHS = {'auto': 0, 'vector': 1, 'mfma': 2}
 
 
 def row_bytes(bits):
@@ -72,11 +76,14 @@ class GPUCache(_CacheBase):
     """Mixed 4/8/16-bit KV cache for batch one and head_dim 64 (src/gpu_cache.py:10-149)."""
 
     def __init__(self, plan=None, layers=30, heads=3, dim=64, device='cuda', dtype=torch.bfloat16,
-                 backend='fused', block_m=16, block_n=64, max_tokens=8192, arena_bytes=None):
+                 backend='fused', block_m=16, block_n=64, max_tokens=8192, arena_bytes=None, precision='bf16'):
         if _CacheBase is not object:
             super().__init__()
         if dim != 64:
             raise ValueError('GPU kernel currently supports head_dim=64')
+        if precision not in PRECISIONS:
+            raise ValueError(f'precision must be one of {sorted(PRECISIONS)}')
+        self.precision = precision
         self.layers, self.heads, self.dim = layers, heads, dim
         self.dtype, self.device = dtype, torch.device(device)
         self.backend, self.block_m, self.block_n = backend, block_m, block_n
@@ -272,7 +279,7 @@ class GPUCache(_CacheBase):
             x = x.to(torch.bfloat16).contiguous()
         return x
 
-    def attend_args(self, q, k, v, layer, past, out, segments=None, path=0, splits=0):
+    def attend_args(self, q, k, v, layer, past, out, segments=None, path=0, splits=0, precision=None):
         """Fills the C argument block of one attention call."""
         nq = q.shape[-2]
         a = _lib.AttnArgs()
@@ -292,20 +299,30 @@ class GPUCache(_CacheBase):
         a.out = out.data_ptr()
         a.out_tok_stride, a.out_head_stride = out.stride(1), out.stride(2)
         a.out_dtype = 1 if out.dtype == torch.float32 else 0
-        a.path, a.splits = path, splits
+        a.path = PATHS[path] if isinstance(path, str) else int(path)
+        a.splits = splits
+        a.precision = PRECISIONS[precision or self.precision]
         return a
 
     def _workspace_for(self, nbytes):
+        # Zero-filled once: the attention kernels keep their arrival counters in it and leave
+        # them zero after every call.
         if self._workspace is None or self._workspace.numel() < nbytes or self._workspace.device != self.device:
-            self._workspace = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=self.device)
+            self._workspace = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=self.device)
         return self._workspace
 
-    def attend(self, q, k, v, layer, past, out_dtype=None, segments=None, path=0, splits=0):
+    def attend(self, q, k, v, layer, past, out_dtype=None, segments=None, path=0, splits=0, precision=None):
         """Causal attention of q over history [0, past) plus the native chunk (src/gpu_cache.py:96-104).
 
         `segments` (optional) lists chunk boundaries [0, b1, ..., nq] for a block-diagonal batch of
-        independent continuations that share the history, e.g. QA candidates.
+        independent continuations that share the history, e.g. QA candidates. `path` is 'auto'
+        (MFMA once a KV head has 16 query rows), 'vector' or 'mfma'; `precision` overrides the
+        cache's 'bf16' / 'fp32' setting for this call.
         """
+        if precision is not None and precision not in PRECISIONS:
+            raise ValueError(f'precision must be one of {sorted(PRECISIONS)}')
+        if isinstance(path, str) and path not in PATHS:
+            raise ValueError(f'path must be one of {sorted(PATHS)}')
         n = q.shape[-2]
         if q.dim() != 4 or q.shape[0] != 1 or q.shape[-1] != self.dim or q.shape[1] % self.heads:
             raise ValueError('attend expects q [1, q_heads, n, 64] with q_heads a multiple of heads')
@@ -317,7 +334,7 @@ class GPUCache(_CacheBase):
             raise ValueError('attend requires CUDA tensors on one device')
         q, k, v = self._kv_view(q), self._kv_view(k), self._kv_view(v)
         out = torch.empty((1, n, q.shape[1], self.dim), dtype=out_dtype or q.dtype, device=q.device)
-        a = self.attend_args(q, k, v, layer, past, out, segments, path, splits)
+        a = self.attend_args(q, k, v, layer, past, out, segments, path, splits, precision)
         lib = _lib.load()
         need = lib.dkv_attend_workspace_bytes(ctypes.byref(a))
         if need:

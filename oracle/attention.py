@@ -55,11 +55,11 @@ def attention(q, k, v, past, scale=0.125, segments=None, dtype=torch.float64):
     return (torch.softmax(s, dim=-1) @ vx).transpose(0, 1).contiguous()
 
 
-def reference_semantics(q, k, v, past, scale=0.125, block=64):
+def reference_semantics(q, k, v, past, scale=0.125, block=64, segments=None, out_dtype=torch.bfloat16):
     """Emulation of the reference kernel's bf16 rounding (src/gpu_kernels.py:84-105).
 
     q [Hq, nq, 64] bf16; k, v [H, past + nq, 64] fp32 (dequantized history, native chunk).
-    Returns [nq, Hq, 64] bf16.
+    Returns [nq, Hq, 64] in out_dtype (the reference stores bf16; fp32 keeps acc / den unrounded).
     """
     hq, nq, _ = q.shape
     g = hq // k.shape[0]
@@ -67,7 +67,7 @@ def reference_semantics(q, k, v, past, scale=0.125, block=64):
     kb = k.to(torch.bfloat16).float().repeat_interleave(g, 0)
     vb = v.to(torch.bfloat16).float().repeat_interleave(g, 0)
     total = past + nq
-    mask = visible_mask(past, nq)
+    mask = visible_mask(past, nq, segments)
     mx = torch.full((hq, nq), float('-inf'))
     den = torch.zeros(hq, nq)
     acc = torch.zeros(hq, nq, 64)
@@ -81,4 +81,4 @@ def reference_semantics(q, k, v, past, scale=0.125, block=64):
         den = den * alpha + p.sum(-1)
         acc = acc * alpha[..., None] + p.to(torch.bfloat16).float() @ vb[:, b0:b1]
         mx = new
-    return (acc / den[..., None]).to(torch.bfloat16).transpose(0, 1).contiguous()
+    return (acc / den[..., None]).to(out_dtype).transpose(0, 1).contiguous()

@@ -1,11 +1,19 @@
-"""Attention parity on the GPU against the CPU oracle.
+"""Attention parity on the GPU against the CPU oracle, for both kernels (MFMA and vector).
 
 Tolerances:
-  fp32 output vs the fp64 dequantize-then-SDPA oracle: max-abs <= 1e-3.
-  bf16 output vs the same oracle: |out - oracle| <= 1e-3 + 2^-8 |oracle| (the bf16 store rounds
-    to nearest, which costs at most half an ulp = 2^-8 relative).
-  bf16 output vs the reference kernel's bf16 semantics on the reference's own test distribution
-    (unit-normal values): max-abs <= 2e-2.
+  precision='fp32', fp32 output vs the fp64 dequantize-then-SDPA oracle: max-abs <= 1e-3.
+  precision='fp32', bf16 output vs the same oracle: |out - oracle| <= 1e-3 + 2^-8 |oracle| (the
+    bf16 store rounds to nearest, at most half an ulp = 2^-8 relative).
+  precision='bf16' (the reference kernel's rounding of K, V and p to bf16) vs the emulated
+    reference kernel (oracle.attention.reference_semantics):
+    - one split (the reference's own key order, so p is rounded against the same running max):
+      fp32 output max-abs <= 2e-2;
+    - the default split history: each split rounds p against its own running max, so the result
+      also carries the reference's own dependence on where its 64-key blocks fall. The bound is
+      2e-2 plus that dependence measured on the same input (reference at 32-key blocks vs 64-key
+      blocks), which is up to 1.5e-2 on the outlier-channel data;
+    - bf16 output: the fp32 bound + 2^-7 |ref|, since two bf16 roundings of nearby values can land
+      one bf16 ulp (2^-7 relative) apart and outlier-channel outputs reach |O| ~ 20 (ulp 0.125).
   The reference's own scenarios keep their tolerances (atol .035, rtol .015; max-abs < .035).
 """
 import pytest
@@ -47,34 +55,92 @@ def oracle_out(case, dk, dv, segments=None):
     return attention(case['q'], k, v, dk.shape[1], segments=segments)
 
 
-def run(c, case, cuda, out_dtype, segments=None, path=0, splits=0):
+def run(c, case, cuda, out_dtype, segments=None, path='auto', splits=0, precision='fp32'):
     q, kn, vn = (case[x][None].to(cuda) for x in ('q', 'k_new', 'v_new'))
     c.select(16)
     past = c.append(kn, vn, 0)
-    out = c.attend(q, kn, vn, 0, past, out_dtype=out_dtype, segments=segments, path=path, splits=splits)
+    out = c.attend(q, kn, vn, 0, past, out_dtype=out_dtype, segments=segments, path=path, splits=splits,
+                   precision=precision)
     torch.cuda.synchronize()
     return out[0].cpu().double()
 
 
+def semantics_out(case, dk, dv, segments=None, out_dtype=torch.bfloat16):
+    k = torch.cat((dk, case['k_new'].float()), 1)
+    v = torch.cat((dv, case['v_new'].float()), 1)
+    return reference_semantics(case['q'], k, v, dk.shape[1], segments=segments, out_dtype=out_dtype).double()
+
+
+def block_sensitivity(case, dk, dv, segments=None):
+    """max |reference(32-key blocks) - reference(64-key blocks)| on this input."""
+    k = torch.cat((dk, case['k_new'].float()), 1)
+    v = torch.cat((dv, case['v_new'].float()), 1)
+    b32 = reference_semantics(case['q'], k, v, dk.shape[1], block=32, segments=segments, out_dtype=torch.float32)
+    b64 = reference_semantics(case['q'], k, v, dk.shape[1], block=64, segments=segments, out_dtype=torch.float32)
+    return (b32 - b64).abs().max().item()
+
+
+def assert_semantics(c, case, dk, dv, cuda, path, segments=None):
+    ref32 = semantics_out(case, dk, dv, segments, torch.float32)
+    q, kn, vn = (case[x][None].to(cuda) for x in ('q', 'k_new', 'v_new'))
+    c.select(16)
+    past = c.append(kn, vn, 0)
+    one = c.attend(q, kn, vn, 0, past, out_dtype=torch.float32, segments=segments, path=path, splits=1,
+                   precision='bf16')[0].cpu().double()
+    err1 = (one - ref32).abs().max().item()
+    assert err1 <= 2e-2, err1
+    tol = 2e-2 + block_sensitivity(case, dk, dv, segments)
+    got = c.attend(q, kn, vn, 0, past, out_dtype=torch.float32, segments=segments, path=path,
+                   precision='bf16')[0].cpu().double()
+    err = (got - ref32).abs().max().item()
+    assert err <= tol, (err, tol)
+    got = c.attend(q, kn, vn, 0, past, segments=segments, path=path, precision='bf16')[0].cpu().double()
+    ref = semantics_out(case, dk, dv, segments)
+    assert torch.all((got - ref).abs() <= tol + ref.abs() * 2.0 ** -7)
+
+
+PATHS = ['mfma', 'vector']
+
+
+@pytest.mark.parametrize('path', PATHS)
 @pytest.mark.parametrize('past', [1024, 4096, 8128])
-def test_frame_chunk_fp32_within_1e3_of_fp64_oracle(cuda, past):
-    announce(f'attention frame chunk past={past} fp32 out')
+def test_frame_chunk_fp32_within_1e3_of_fp64_oracle(cuda, past, path):
+    announce(f'attention frame chunk past={past} path={path} precision=fp32 fp32 out')
     case = frame_chunk_case(past, seed=past)
     c, dk, dv = build(case, cuda)
-    got = run(c, case, cuda, torch.float32)
+    got = run(c, case, cuda, torch.float32, path=path)
     ref = oracle_out(case, dk, dv)
     err = (got - ref).abs().max().item()
     assert err <= 1e-3, err
 
 
+@pytest.mark.parametrize('path', PATHS)
 @pytest.mark.parametrize('past', [1024, 8128])
-def test_frame_chunk_bf16_faithfully_rounded(cuda, past):
-    announce(f'attention frame chunk past={past} bf16 out')
+def test_frame_chunk_bf16_faithfully_rounded(cuda, past, path):
+    announce(f'attention frame chunk past={past} path={path} precision=fp32 bf16 out')
     case = frame_chunk_case(past, seed=past + 1)
     c, dk, dv = build(case, cuda)
-    got = run(c, case, cuda, torch.bfloat16)
+    got = run(c, case, cuda, torch.bfloat16, path=path)
     ref = oracle_out(case, dk, dv)
     assert torch.all((got - ref).abs() <= 1e-3 + ref.abs() * 2.0 ** -8)
+
+
+@pytest.mark.parametrize('path', PATHS)
+@pytest.mark.parametrize('past', [1024, 4096, 8128])
+def test_frame_chunk_bf16_semantics_within_2e2_of_reference(cuda, past, path):
+    announce(f'attention frame chunk past={past} path={path} precision=bf16')
+    case = frame_chunk_case(past, seed=past + 2)
+    c, dk, dv = build(case, cuda)
+    assert_semantics(c, case, dk, dv, cuda, path)
+
+
+@pytest.mark.parametrize('path', PATHS)
+@pytest.mark.parametrize('bits', [4, 8])
+def test_candidates_bf16_semantics_within_2e2_of_reference(cuda, bits, path):
+    announce(f'attention candidates bits={bits} path={path} precision=bf16')
+    case = candidate_case(bits, seed=3, past=6144)
+    c, dk, dv = build(case, cuda)
+    assert_semantics(c, case, dk, dv, cuda, path, case['segments'])
 
 
 def test_bf16_within_2e2_of_reference_semantics_on_unit_normal_data(cuda):
@@ -88,54 +154,59 @@ def test_bf16_within_2e2_of_reference_semantics_on_unit_normal_data(cuda):
                 v_new=torch.randn(5, nq, 64, generator=g).bfloat16(),
                 bits=[4, 8, 16, 4] * 4)
     c, dk, dv = build(case, cuda)
-    got = run(c, case, cuda, torch.bfloat16)
+    got = run(c, case, cuda, torch.bfloat16, precision='bf16')
     k = torch.cat((dk, case['k_new'].float()), 1)
     v = torch.cat((dv, case['v_new'].float()), 1)
     ref = reference_semantics(case['q'], k, v, past).double()
     assert (got - ref).abs().max().item() <= 2e-2
 
 
-def test_plan_mode_and_partial_tiles(cuda):
-    announce('attention plan mode, partial tiles')
+@pytest.mark.parametrize('path', PATHS)
+def test_plan_mode_and_partial_tiles(cuda, path):
+    announce(f'attention plan mode, partial tiles, path={path}')
     case = frame_chunk_case(1000, seed=5, nq=37)
     c, dk, dv = build(case, cuda, plan_mode=True)
-    got = run(c, case, cuda, torch.float32)
+    got = run(c, case, cuda, torch.float32, path=path)
     assert (got - oracle_out(case, dk, dv)).abs().max().item() <= 1e-3
 
 
+@pytest.mark.parametrize('path', ['auto', 'mfma'])
 @pytest.mark.parametrize('nq', [1, 5, 16, 77, 130])
-def test_chunk_lengths(cuda, nq):
-    announce(f'attention nq={nq}')
+def test_chunk_lengths(cuda, nq, path):
+    announce(f'attention nq={nq} path={path}')
     case = frame_chunk_case(640, seed=nq, nq=nq)
     c, dk, dv = build(case, cuda)
-    got = run(c, case, cuda, torch.float32)
+    got = run(c, case, cuda, torch.float32, path=path)
     assert (got - oracle_out(case, dk, dv)).abs().max().item() <= 1e-3
 
 
+@pytest.mark.parametrize('path', PATHS)
 @pytest.mark.parametrize('splits', [1, 3, 1000])
-def test_split_counts_agree(cuda, splits):
-    announce(f'attention splits={splits}')
+def test_split_counts_agree(cuda, splits, path):
+    announce(f'attention splits={splits} path={path}')
     case = frame_chunk_case(2048, seed=3)
     c, dk, dv = build(case, cuda)
-    got = run(c, case, cuda, torch.float32, splits=splits)
+    got = run(c, case, cuda, torch.float32, splits=splits, path=path)
     assert (got - oracle_out(case, dk, dv)).abs().max().item() <= 1e-3
 
 
+@pytest.mark.parametrize('path', PATHS)
 @pytest.mark.parametrize('bits', [4, 8])
-def test_candidates_block_diagonal(cuda, bits):
-    announce(f'attention candidates bits={bits}')
+def test_candidates_block_diagonal(cuda, bits, path):
+    announce(f'attention candidates bits={bits} path={path}')
     case = candidate_case(bits, seed=2, past=1536)
     c, dk, dv = build(case, cuda)
-    got = run(c, case, cuda, torch.float32, segments=case['segments'])
+    got = run(c, case, cuda, torch.float32, segments=case['segments'], path=path)
     ref = oracle_out(case, dk, dv, segments=case['segments'])
     assert (got - ref).abs().max().item() <= 1e-3
 
 
-def test_empty_history(cuda):
-    announce('attention past=0')
+@pytest.mark.parametrize('path', PATHS)
+def test_empty_history(cuda, path):
+    announce(f'attention past=0 path={path}')
     case = frame_chunk_case(0, seed=1, nq=70)
     c = GPUCache(None, layers=1, heads=5, max_tokens=256)
-    got = run(c, case, cuda, torch.float32)
+    got = run(c, case, cuda, torch.float32, path=path)
     ref = oracle_out(case, case['k_hist'].float(), case['v_hist'].float())
     assert (got - ref).abs().max().item() <= 1e-3
 

@@ -105,3 +105,56 @@ def test_reference_scenario_semantics_within_reference_tolerance(query_length):
     exact = attention(q, k, v, past=hk.shape[1])
     emulated = reference_semantics(q, k, v, past=hk.shape[1])
     assert torch.allclose(emulated.double(), exact, atol=.035, rtol=.015)
+
+
+def _closed_form(q, k, v, past):
+    """bf16(exp(s - max)) @ bf16(V) / sum(exp(s - max)), one pass over all keys."""
+    g = q.shape[0] // k.shape[0]
+    kb = k.bfloat16().float().repeat_interleave(g, 0)
+    vb = v.bfloat16().float().repeat_interleave(g, 0)
+    s = (q.float() @ kb.transpose(1, 2)) * 0.125
+    s = s.masked_fill(~visible_mask(past, q.shape[1]), float('-inf'))
+    p = torch.exp(s - s.amax(-1, keepdim=True))
+    return ((p.bfloat16().float() @ vb) / p.sum(-1, keepdim=True)).transpose(0, 1), s
+
+
+def test_reference_semantics_one_block_closed_form():
+    # One block over every key: the emulation is exactly the closed form, and the rounding
+    # points are really there (it differs from the unrounded fp32 result).
+    g = torch.Generator().manual_seed(31)
+    q = torch.randn(6, 5, 64, generator=g).bfloat16()
+    k = torch.randn(2, 155, 64, generator=g)
+    v = torch.randn(2, 155, 64, generator=g)
+    got = reference_semantics(q, k, v, 150, block=256, out_dtype=torch.float32)
+    expect, _ = _closed_form(q, k, v, 150)
+    assert torch.allclose(got, expect, rtol=1e-6, atol=1e-6)
+    assert (got - attention(q, k, v, 150, dtype=torch.float32)).abs().max() > 1e-4
+
+
+def test_reference_semantics_blocks_without_rescaling():
+    # When the first 64-key block holds every row's maximum, the online loop never rescales and
+    # must equal the closed form even with 64-key blocks.
+    g = torch.Generator().manual_seed(33)
+    q = (torch.randn(6, 5, 64, generator=g) + 2).bfloat16()
+    k = torch.randn(2, 155, 64, generator=g)
+    k[:, 0] = 0.5
+    k[:, 64:] *= 0.1
+    v = torch.randn(2, 155, 64, generator=g)
+    got = reference_semantics(q, k, v, 150, out_dtype=torch.float32)
+    expect, s = _closed_form(q, k, v, 150)
+    assert torch.equal(s.argmax(-1), torch.zeros(6, 5, dtype=torch.long))
+    assert torch.allclose(got, expect, rtol=1e-6, atol=1e-6)
+
+
+def test_reference_semantics_segments_equal_separate_calls():
+    g = torch.Generator().manual_seed(32)
+    past, bounds = 70, [0, 4, 9]
+    q = torch.randn(3, 9, 64, generator=g).bfloat16()
+    k = torch.randn(1, past + 9, 64, generator=g)
+    v = torch.randn(1, past + 9, 64, generator=g)
+    got = reference_semantics(q, k, v, past, segments=bounds, out_dtype=torch.float32)
+    for lo, hi in ((0, 4), (4, 9)):
+        kc = torch.cat((k[:, :past], k[:, past + lo:past + hi]), 1)
+        vc = torch.cat((v[:, :past], v[:, past + lo:past + hi]), 1)
+        alone = reference_semantics(q[:, lo:hi], kc, vc, past, out_dtype=torch.float32)
+        assert torch.allclose(got[lo:hi], alone, atol=1e-6)
