@@ -59,7 +59,23 @@ def pack_bytes(bits, layers=LAYERS, heads=HEADS, tile=TILE):
     return read, write
 
 
-def bench_pack(steps, warmup):
+def graph_of(fn, reps):
+    """A HIP graph that runs fn() `reps` times back to back (captured on torch's stream)."""
+    import torch
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            fn()
+    torch.cuda.synchronize()
+    return graph
+
+
+def bench_pack(steps, warmup, reps=10):
+    """One step = one launch packing the whole volume; timed as graph replays of `reps` launches."""
     import torch
     from dkv.gpu_cache import GPUCache
     from dkv.workloads import pack_volume
@@ -68,10 +84,23 @@ def bench_pack(steps, warmup):
     k, v = vol['k'].to(dev), vol['v'].to(dev)
     cache = GPUCache(None, layers=LAYERS, heads=HEADS, max_tokens=96 * TILE)
     batch = cache.append_batch(k, v, vol['bits'], [TILE] * 96)
-    ms = time_launches(batch.run, steps, warmup)
+    graph = graph_of(batch.run, reps)
+    rounds = max(1, steps // reps)
+    ms = time_launches(graph.replay, rounds, max(1, warmup // reps)) / reps
     read, write = pack_bytes(vol['bits'])
     gbs = (read + write) / (ms * 1e-3) / 1e9
-    return dict(ms=ms, gbs=gbs, read_bytes=read, write_bytes=write, bits=vol['bits'])
+    return dict(ms=ms, gbs=gbs, read_bytes=read, write_bytes=write, bits=vol['bits'], steps=rounds * reps)
+
+
+def bench_copy(steps, nbytes=256 << 20, reps=10):
+    """Device-to-device copy of nbytes (torch copy_): the attainable streaming rate, read + write."""
+    import torch
+    dev = torch.device('cuda:0')
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    graph = graph_of(lambda: dst.copy_(src), reps)
+    ms = time_launches(graph.replay, max(1, steps // reps), 1) / reps
+    return dict(ms=ms, gbs=2 * nbytes / (ms * 1e-3) / 1e9, bytes=nbytes)
 
 
 def attention_setup(past, rotate, bits, nq=64, segments=None, seed=0, precision='bf16', path='auto', splits=0):
@@ -220,6 +249,8 @@ def main():
     if args.only in ('pack', 'all'):
         res['pack'] = bench_pack(args.steps, args.warmup)
         print(f"# pack: {res['pack']['ms'] * 1e3:.1f} us/launch, {res['pack']['gbs']:.0f} GB/s", flush=True)
+        res['copy'] = bench_copy(args.steps)
+        print(f"# copy 256 MiB: {res['copy']['ms'] * 1e3:.1f} us, {res['copy']['gbs']:.0f} GB/s", flush=True)
     if args.only in ('attn', 'all'):
         res['attention'] = {}
         for prec in ('bf16', 'fp32'):
@@ -240,7 +271,8 @@ def main():
     p = res.get('pack')
     line = dict(
         metric='packed-KV attn us/layer + HBM GB/s @8k mixed history; pack GB/s; frames/s e2e',
-        value=round(p['gbs'], 2) if p else None, unit='GB/s', n_gpus=1, steps=args.steps, warmup=args.warmup,
+        value=round(p['gbs'], 2) if p else None, unit='GB/s', n_gpus=1, steps=p['steps'] if p else args.steps,
+        warmup=args.warmup,
         ms_per_step=round(p['ms'], 5) if p else None, higher_is_better=True, scaling='weak', vs_baseline=None,
         dtype='bf16->u4/u8/bf16', data='synthetic',
         config=dict(workload='pack: 32 layers x 5 KV heads x 6144 tokens (96 tiles of 64) bf16 K+V, '
@@ -249,6 +281,7 @@ def main():
     if p:
         line['roofline'] = dict(bound='hbm', achieved=round(p['gbs'], 1), peak=HBM_PEAK_GBS,
                                 unit='GB/s', frac=round(p['gbs'] / HBM_PEAK_GBS, 4), traffic=None)
+        line['copy_reference_gbs'] = round(res['copy']['gbs'], 1)
     if 'attention' in res:
         line['attention'] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in r.items()}
                              for k, r in res['attention'].items()}

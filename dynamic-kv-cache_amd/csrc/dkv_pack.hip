@@ -7,13 +7,22 @@
 // (src/kv_quantization.py:57-71, src/gpu_kernels.py:19-46):
 //   a = min(x); span = max(x) - a; s = span > 0 ? span / (2^b - 1) : 1
 //   q = clamp(rint((x - a) / s), 0, 2^b - 1)
-// with IEEE fp32 subtraction and correctly rounded division (the build passes
-// -ffp-contract=off and -fhip-fp32-correctly-rounded-divide-sqrt).
+// with IEEE fp32 subtraction and division (the build passes -ffp-contract=off
+// and -fhip-fp32-correctly-rounded-divide-sqrt).
 //
-// Launch shape: two threads per row, 32 elements (64 bytes, four 128-bit loads)
-// each, so one 256-thread workgroup streams 128 rows. The only cross-lane step
-// is one min/max exchange between the two halves of a row. Stores are 128-bit:
-// a half row of 4-bit codes is exactly 16 bytes, of 8-bit codes 2 x 16 bytes.
+// The per-element division is the expensive part (about ten VALU operations
+// when correctly rounded), so the kernel first forms t = (x - a) * rcp(s). For
+// 0 <= (x - a)/s <= 256, v_rcp_f32 (1 ulp) and the product put t within
+// 2^-14.3 of the exact quotient and the correctly rounded quotient within
+// 2^-16 of it, so both round to the same integer unless t is within 2^-13 of a
+// half-integer. Those rows (and any row whose t is not finite, e.g. a
+// subnormal scale) take the correctly rounded division instead; the result is
+// bit-identical to rint((x - a) / s) in every case.
+//
+// Launch shape: one wave packs 64 consecutive tokens of one (K or V, head) of
+// one job. Global loads and stores are 16 bytes per lane over contiguous
+// rows; an LDS transpose hands each lane one whole row, so a row's min/max,
+// scale and reciprocal are computed once.
 #include "dkv_common.h"
 #include <stdarg.h>
 #include <stdio.h>
@@ -31,89 +40,178 @@ void set_error(const char* fmt, ...) {
 }
 void clear_error() { g_err[0] = 0; }
 
-constexpr int PACK_THREADS = 256;
-constexpr int PACK_ROWS_PER_BLOCK = PACK_THREADS / 2;
+constexpr int PACK_THREADS = 256;  // 4 waves
+constexpr int WAVE_ROWS = 64;      // tokens of one (kv, head) per wave, one per lane
+constexpr float TIE_GUARD = 0.5f - 0x1p-13f;
 
-struct Half32 {
-  float x[32];
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x8_t __attribute__((ext_vector_type(8)));
+
+struct RowDst {
+  uint8_t* payload;  // start of the row's payload
+  float2* meta;      // the row's (offset, scale)
 };
 
-__device__ __forceinline__ void load_half_row(const uint16_t* src, Half32& h) {
-  const u32x4* p = reinterpret_cast<const u32x4*>(src);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const u32x4 w = __builtin_nontemporal_load(p + i);
-    h.x[8 * i + 0] = bf16_lo(w.x);
-    h.x[8 * i + 1] = bf16_hi(w.x);
-    h.x[8 * i + 2] = bf16_lo(w.y);
-    h.x[8 * i + 3] = bf16_hi(w.y);
-    h.x[8 * i + 4] = bf16_lo(w.z);
-    h.x[8 * i + 5] = bf16_hi(w.z);
-    h.x[8 * i + 6] = bf16_lo(w.w);
-    h.x[8 * i + 7] = bf16_hi(w.w);
-  }
+__device__ __forceinline__ RowDst row_dst(const dkv_pack_job& j, int kv, int head, int tok, uint8_t* arena,
+                                          int layers, int heads) {
+  const int r_seg = j.row0 + tok;
+  const int ti = r_seg / TILE;
+  const int rt = r_seg - ti * TILE;
+  const int rows_i = min(TILE, j.seg_rows - ti * TILE);
+  const int64_t sb = subblock_bytes(rows_i, j.bits);
+  uint8_t* sub = arena + j.seg_offset + (int64_t)ti * slab_bytes(TILE, j.bits, layers, heads) +
+                 ((int64_t)(j.layer * 2 + kv) * heads + head) * sb;
+  RowDst d;
+  d.payload = sub + (int64_t)rt * row_bytes(j.bits);
+  d.meta = reinterpret_cast<float2*>(sub + (int64_t)rows_i * row_bytes(j.bits)) + rt;
+  return d;
 }
 
-// Packs one 64-element row, of which this thread holds half `half` (0/1).
-// `src` points at the thread's 32 input elements; the partner thread is the
-// adjacent lane (lane ^ 1).
-__device__ __forceinline__ void pack_half_row(const uint16_t* src, int half, int bits,
-                                              uint8_t* payload_row, float2* meta_row) {
-  if (bits == 16) {
-    const u32x4* p = reinterpret_cast<const u32x4*>(src);
-    u32x4* o = reinterpret_cast<u32x4*>(payload_row + half * 64);
+// Quantizes 8 elements of a row whose (offset, scale) is (a, s) and 1/s ~ r.
+template <int BITS>
+__device__ __forceinline__ void quantize8(const float* x, float a, float s, float r, float* q) {
+  constexpr float LEVELS = BITS == 4 ? 15.0f : 255.0f;
+  bool ok = true;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = __builtin_nontemporal_load(p + i);
+  for (int e = 0; e < 8; ++e) {
+    const float t = (x[e] - a) * r;
+    q[e] = rintf(t);
+    ok = ok && fabsf(t - q[e]) < TIE_GUARD;  // false for non-finite t
+  }
+  if (!ok) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q[e] = rintf(__fdiv_rn(x[e] - a, s));
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) q[e] = __builtin_amdgcn_fmed3f(q[e], 0.0f, LEVELS);
+}
+
+// A wave packs 64 rows (one per lane) staged through LDS: lanes load and store
+// global memory 16 bytes each, 8 lanes per row (every instruction covers 1 KB
+// of contiguous rows), while the arithmetic runs one row per lane, so a row's
+// min/max, scale and reciprocal are computed once. LDS rows are padded to
+// 144 bytes, which makes both the 8-lanes-per-row and the lane-per-row
+// accesses conflict-free.
+constexpr int LROW = 144;                  // padded LDS row, bytes
+constexpr int WAVE_LDS = WAVE_ROWS * LROW;  // 9216 bytes per wave
+
+template <int BITS>
+__device__ __forceinline__ void pack_wave(const dkv_pack_job& j, int kv, int head, int tok0, uint8_t* arena,
+                                          int layers, int heads, uint8_t* lds) {
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 7;
+  const uint16_t* base = kv == 0 ? static_cast<const uint16_t*>(j.k) + head * j.k_head_stride
+                                 : static_cast<const uint16_t*>(j.v) + head * j.v_head_stride;
+  const int64_t ts = kv == 0 ? j.k_tok_stride : j.v_tok_stride;
+  const int nrows = min(WAVE_ROWS, j.n - tok0);
+  // Destination: one wave-uniform sub-block base when the wave's rows sit in
+  // one tile (every append that starts on a tile boundary).
+  const int rfirst = j.row0 + tok0;
+  const int rlast = rfirst + nrows - 1;
+  const bool one_tile = rfirst / TILE == rlast / TILE;
+  const RowDst d0 = row_dst(j, kv, head, tok0, arena, layers, heads);
+  constexpr int RB = BITS == 4 ? 32 : (BITS == 8 ? 64 : 128);
+
+  u32x4 w[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = 8 * i + (lane >> 3);
+    w[i] = r < nrows ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + (tok0 + r) * ts + 8 * c))
+                     : u32x4{0, 0, 0, 0};
+  }
+  if (BITS == 16) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = 8 * i + (lane >> 3);
+      if (r >= nrows) continue;
+      uint8_t* dst = one_tile ? d0.payload + r * 128 : row_dst(j, kv, head, tok0 + r, arena, layers, heads).payload;
+      __builtin_nontemporal_store(w[i], reinterpret_cast<u32x4*>(dst + 16 * c));
+    }
     return;
   }
-  Half32 h;
-  load_half_row(src, h);
-  float lo = h.x[0], hi = h.x[0];
 #pragma unroll
-  for (int i = 1; i < 32; ++i) {
-    lo = fminf(lo, h.x[i]);
-    hi = fmaxf(hi, h.x[i]);
+  for (int i = 0; i < 8; ++i)
+    *reinterpret_cast<u32x4*>(lds + (8 * i + (lane >> 3)) * LROW + 16 * c) = w[i];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float x[64];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(lds + lane * LROW + 16 * i);
+    const f32x8_t f = __builtin_convertvector(__builtin_bit_cast(bf16x8_t, v), f32x8_t);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[8 * i + e] = f[e];
   }
-  lo = fminf(lo, __shfl_xor(lo, 1));
-  hi = fmaxf(hi, __shfl_xor(hi, 1));
+  float lo = x[0], hi = x[0];
+#pragma unroll
+  for (int e = 1; e < 64; ++e) {
+    lo = fminf(lo, x[e]);
+    hi = fmaxf(hi, x[e]);
+  }
   const float a = lo;
   const float span = hi - a;
-  const float levels = bits == 4 ? 15.0f : 255.0f;
-  const float s = span > 0.0f ? span / levels : 1.0f;
-  uint32_t q[32];
+  const float s = span > 0.0f ? __fdiv_rn(span, BITS == 4 ? 15.0f : 255.0f) : 1.0f;
+  const float rs = __builtin_amdgcn_rcpf(s);
+  uint32_t out[RB / 4];
 #pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    float v = rintf((h.x[i] - a) / s);
-    v = fminf(fmaxf(v, 0.0f), levels);
-    q[i] = (uint32_t)v;
-  }
-  if (bits == 4) {
-    uint32_t w[4];
+  for (int i = 0; i < 8; ++i) {
+    float q[8];
+    quantize8<BITS>(x + 8 * i, a, s, rs, q);
+    if (BITS == 4) {
+      uint32_t word = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      uint32_t acc = 0;
+      for (int e = 0; e < 8; ++e) word |= (uint32_t)q[e] << (4 * e);
+      out[i] = word;
+    } else {
+      uint32_t w0 = 0, w1 = 0;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc |= q[8 * i + j] << (4 * j);
-      w[i] = acc;
+      for (int e = 0; e < 4; ++e) {
+        w0 |= (uint32_t)q[e] << (8 * e);
+        w1 |= (uint32_t)q[4 + e] << (8 * e);
+      }
+      out[2 * i] = w0;
+      out[2 * i + 1] = w1;
     }
-    *reinterpret_cast<uint4*>(payload_row + half * 16) = make_uint4(w[0], w[1], w[2], w[3]);
-  } else {
-    uint32_t w[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      w[i] = q[4 * i] | (q[4 * i + 1] << 8) | (q[4 * i + 2] << 16) | (q[4 * i + 3] << 24);
-    uint4* o = reinterpret_cast<uint4*>(payload_row + half * 32);
-    o[0] = make_uint4(w[0], w[1], w[2], w[3]);
-    o[1] = make_uint4(w[4], w[5], w[6], w[7]);
   }
-  if (half == 0) *meta_row = make_float2(a, s);
+  const bool valid = lane < nrows;
+  if (!one_tile) {  // rows straddle a tile boundary: each lane stores its own row
+    if (valid) {
+      const RowDst d = row_dst(j, kv, head, tok0 + lane, arena, layers, heads);
+#pragma unroll
+      for (int i = 0; i < RB / 16; ++i)
+        *reinterpret_cast<u32x4*>(d.payload + 16 * i) = u32x4{out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]};
+      *d.meta = make_float2(a, s);
+    }
+    return;
+  }
+  if (valid) d0.meta[lane] = make_float2(a, s);
+  // Packed rows back through LDS (the wave's own region, already read), then
+  // contiguous 16-byte stores: RB bytes per row, rows back to back.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+  for (int i = 0; i < RB / 16; ++i)
+    *reinterpret_cast<u32x4*>(lds + lane * RB + 16 * i) = u32x4{out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]};
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int bytes = nrows * RB;
+#pragma unroll
+  for (int i = 0; i < RB / 16; ++i) {
+    const int off = 16 * (lane + 64 * i);
+    if (off < bytes)
+      __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(lds + off), reinterpret_cast<u32x4*>(d0.payload + off));
+  }
 }
 
+// Tile descriptors of the job's segment, written by the lanes of one wave.
 __device__ __forceinline__ void write_segment_tiles(const dkv_pack_job& j, int layers, int heads,
                                                     dkv_tile* tiles) {
   const int ntiles = (j.seg_rows + TILE - 1) / TILE;
   const int64_t full = slab_bytes(TILE, j.bits, layers, heads);
-  for (int t = threadIdx.x; t < ntiles; t += blockDim.x) {
+  for (int t = threadIdx.x & 63; t < ntiles; t += 64) {
     dkv_tile d;
     d.offset = j.seg_offset + (int64_t)t * full;
     d.token_start = j.seg_token_start + t * TILE;
@@ -125,45 +223,49 @@ __device__ __forceinline__ void write_segment_tiles(const dkv_pack_job& j, int l
   }
 }
 
-__device__ __forceinline__ void pack_job_rows(const dkv_pack_job& j, int block, uint8_t* arena,
-                                              int layers, int heads) {
-  const int rows_total = 2 * heads * j.n;
-  const int row = block * PACK_ROWS_PER_BLOCK + (threadIdx.x >> 1);
-  const int half = threadIdx.x & 1;
-  if (row >= rows_total) return;  // both halves of a row exit together
-  const int per_kv = heads * j.n;
-  const int kv = row / per_kv;
-  const int rem = row - kv * per_kv;
-  const int head = rem / j.n;
-  const int tok = rem - head * j.n;
-  const uint16_t* src = kv == 0
-      ? static_cast<const uint16_t*>(j.k) + head * j.k_head_stride + (int64_t)tok * j.k_tok_stride
-      : static_cast<const uint16_t*>(j.v) + head * j.v_head_stride + (int64_t)tok * j.v_tok_stride;
-  src += half * 32;
-  const int r_seg = j.row0 + tok;
-  const int ti = r_seg / TILE;
-  const int rt = r_seg - ti * TILE;
-  const int rows_i = min(TILE, j.seg_rows - ti * TILE);
-  const int64_t sb = subblock_bytes(rows_i, j.bits);
-  uint8_t* sub = arena + j.seg_offset + (int64_t)ti * slab_bytes(TILE, j.bits, layers, heads) +
-                 ((int64_t)(j.layer * 2 + kv) * heads + head) * sb;
-  uint8_t* payload_row = sub + (int64_t)rt * row_bytes(j.bits);
-  float2* meta_row = reinterpret_cast<float2*>(sub + (int64_t)rows_i * row_bytes(j.bits)) + rt;
-  pack_half_row(src, half, j.bits, payload_row, meta_row);
+// Wave index -> (kv, head, 64-token slice) of the job; the bit width is
+// uniform per job, so the branch below is uniform per wave.
+__device__ __forceinline__ void pack_job_wave(const dkv_pack_job& j, int wave, uint8_t* arena, int layers,
+                                              int heads) {
+  __shared__ __attribute__((aligned(16))) uint8_t stage[PACK_THREADS / 64][WAVE_LDS];
+  uint8_t* lds = stage[(threadIdx.x >> 6)];
+  const int slices = (j.n + WAVE_ROWS - 1) / WAVE_ROWS;
+  const int per_kv = heads * slices;
+  if (wave >= 2 * per_kv) return;
+  const int kv = wave / per_kv;
+  const int rem = wave - kv * per_kv;
+  const int head = rem / slices;
+  const int tok0 = (rem - head * slices) * WAVE_ROWS;
+  if (j.bits == 4) pack_wave<4>(j, kv, head, tok0, arena, layers, heads, lds);
+  else if (j.bits == 8) pack_wave<8>(j, kv, head, tok0, arena, layers, heads, lds);
+  else pack_wave<16>(j, kv, head, tok0, arena, layers, heads, lds);
 }
 
 __global__ void __launch_bounds__(PACK_THREADS)
 pack_one_kernel(dkv_pack_job j, uint8_t* arena, dkv_tile* tiles, int layers, int heads) {
-  if (j.write_tiles && blockIdx.x == 0) write_segment_tiles(j, layers, heads, tiles);
-  pack_job_rows(j, blockIdx.x, arena, layers, heads);
+  const int wave = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * (PACK_THREADS / 64) + (threadIdx.x >> 6)));
+  if (j.write_tiles && wave == 0) write_segment_tiles(j, layers, heads, tiles);
+  pack_job_wave(j, wave, arena, layers, heads);
 }
 
+// Waves are numbered across the whole batch (wpj waves per job, from the
+// largest job), so no workgroup carries idle waves past the end of a job.
 __global__ void __launch_bounds__(PACK_THREADS)
-pack_batch_kernel(const dkv_pack_job* __restrict__ jobs, uint8_t* arena, dkv_tile* tiles,
+pack_batch_kernel(const dkv_pack_job* __restrict__ jobs, int n_jobs, int wpj, uint8_t* arena, dkv_tile* tiles,
                   int layers, int heads) {
-  const dkv_pack_job j = jobs[blockIdx.y];
-  if (j.write_tiles && blockIdx.x == 0) write_segment_tiles(j, layers, heads, tiles);
-  pack_job_rows(j, blockIdx.x, arena, layers, heads);
+  const int gw = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * (PACK_THREADS / 64) + (threadIdx.x >> 6)));
+  const int ji = gw / wpj;
+  if (ji >= n_jobs) return;
+  const dkv_pack_job j = jobs[ji];
+  const int wave = gw - ji * wpj;
+  if (j.write_tiles && wave == 0) write_segment_tiles(j, layers, heads, tiles);
+  pack_job_wave(j, wave, arena, layers, heads);
+}
+
+static int pack_waves(int n, int heads) { return 2 * heads * ((n + WAVE_ROWS - 1) / WAVE_ROWS); }
+
+static int pack_blocks(int n, int heads) {
+  return (pack_waves(n, heads) + PACK_THREADS / 64 - 1) / (PACK_THREADS / 64);
 }
 
 // Reconstruct: one 256-thread block per (tile, kv*heads + head); four threads
@@ -287,8 +389,7 @@ int dkv_pack(const dkv_pack_job* job, void* arena, int64_t arena_bytes, dkv_tile
     set_error("dkv_pack: write_tiles needs a tile table");
     return DKV_EINVAL;
   }
-  const int rows = 2 * heads * job->n;
-  const int blocks = (rows + PACK_ROWS_PER_BLOCK - 1) / PACK_ROWS_PER_BLOCK;
+  const int blocks = pack_blocks(job->n, heads);
   const int grid = blocks > 0 ? blocks : (job->write_tiles ? 1 : 0);
   if (grid == 0) return 0;
   hipLaunchKernelGGL(pack_one_kernel, dim3(grid), dim3(PACK_THREADS), 0, (hipStream_t)stream, *job,
@@ -300,15 +401,16 @@ int dkv_pack_batch(const dkv_pack_job* jobs, int32_t n_jobs, int32_t max_n, void
                    int64_t arena_bytes, dkv_tile* tiles, int32_t layers, int32_t heads, void* stream) {
   clear_error();
   (void)arena_bytes;  // jobs live in device memory; the host validated them when it built them
-  if (!jobs || !arena || n_jobs < 0 || max_n < 0 || layers <= 0 || heads <= 0 || n_jobs > 65535) {
+  if (!jobs || !arena || n_jobs < 0 || max_n < 0 || layers <= 0 || heads <= 0 ||
+      (int64_t)n_jobs * pack_waves(max_n > 0 ? max_n : 1, heads) > INT32_MAX / 2) {
     set_error("dkv_pack_batch: bad arguments (jobs %p, n_jobs %d, max_n %d)", (const void*)jobs, n_jobs, max_n);
     return DKV_EINVAL;
   }
   if (n_jobs == 0) return 0;
-  const int rows = 2 * heads * max_n;
-  const int blocks = (rows + PACK_ROWS_PER_BLOCK - 1) / PACK_ROWS_PER_BLOCK;
-  hipLaunchKernelGGL(pack_batch_kernel, dim3(blocks > 0 ? blocks : 1, n_jobs), dim3(PACK_THREADS), 0,
-                     (hipStream_t)stream, jobs, static_cast<uint8_t*>(arena), tiles, layers, heads);
+  const int wpj = pack_waves(max_n > 0 ? max_n : 1, heads);
+  const int64_t blocks = ((int64_t)n_jobs * wpj + PACK_THREADS / 64 - 1) / (PACK_THREADS / 64);
+  hipLaunchKernelGGL(pack_batch_kernel, dim3((unsigned)blocks), dim3(PACK_THREADS), 0, (hipStream_t)stream, jobs,
+                     n_jobs, wpj, static_cast<uint8_t*>(arena), tiles, layers, heads);
   return (int)hipGetLastError();
 }
 
