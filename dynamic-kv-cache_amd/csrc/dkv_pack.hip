@@ -414,6 +414,23 @@ int dkv_pack_batch(const dkv_pack_job* jobs, int32_t n_jobs, int32_t max_n, void
   return (int)hipGetLastError();
 }
 
+int dkv_pack_validate(const dkv_pack_job* jobs, int32_t n_jobs, int64_t arena_bytes, int32_t layers,
+                      int32_t heads) {
+  clear_error();
+  if ((!jobs && n_jobs > 0) || n_jobs < 0) {
+    set_error("dkv_pack_validate: bad job array");
+    return DKV_EINVAL;
+  }
+  for (int i = 0; i < n_jobs; ++i) {
+    if (int rc = check_job(jobs[i], arena_bytes, layers, heads)) return rc;
+    if (jobs[i].write_tiles && jobs[i].tile_index0 < 0) {
+      set_error("dkv_pack_validate: job %d writes tiles at a negative index", i);
+      return DKV_EINVAL;
+    }
+  }
+  return 0;
+}
+
 int dkv_reconstruct(const void* arena, const dkv_tile* tiles, int32_t n_tiles, int32_t n_tokens,
                     int32_t layer, int32_t layers, int32_t heads, void* out, int32_t out_dtype,
                     void* stream) {

@@ -406,6 +406,9 @@ class PackBatch:
     def __init__(self, cache, jobs, max_n, keep=()):
         self.cache, self.max_n, self.n_jobs, self._keep = cache, max_n, len(jobs), keep
         table = (_lib.PackJob * len(jobs))(*jobs)
+        # the kernel trusts the device table: check the host copy against the arena first
+        _lib.check(_lib.load().dkv_pack_validate(ctypes.addressof(table), len(jobs), cache.arena_bytes,
+                                                 cache.layers, cache.heads), 'dkv_pack_validate')
         raw = torch.frombuffer(bytearray(bytes(table)), dtype=torch.uint8)
         self.table = raw.to(cache.device)
         self.arena, self.arena_bytes, self.tiles = cache.arena, cache.arena_bytes, cache.tiles

@@ -114,13 +114,20 @@ int64_t dkv_slab_bytes(int32_t rows, int32_t bits, int32_t layers, int32_t heads
 int dkv_pack(const dkv_pack_job* job, void* arena, int64_t arena_bytes,
              dkv_tile* tiles, int32_t layers, int32_t heads, void* stream);
 
-/* Pack n_jobs appends in one launch. `jobs` is a DEVICE array. max_n bounds
+/* Pack n_jobs appends in one launch. `jobs` is a DEVICE array that the kernel
+ * trusts: validate its host copy with dkv_pack_validate first. max_n bounds
  * every job's n. There is no reference counterpart for batching: it is the
  * whole-volume form of dkv_pack used when many (layer, frame) tiles are ready
  * at once, e.g. a prefill of several frames. */
 int dkv_pack_batch(const dkv_pack_job* jobs, int32_t n_jobs, int32_t max_n,
                    void* arena, int64_t arena_bytes, dkv_tile* tiles,
                    int32_t layers, int32_t heads, void* stream);
+
+/* Checks a HOST copy of a job table against the arena (what dkv_pack checks for
+ * one job), so that a table can be validated before it is copied to the device
+ * and launched with dkv_pack_batch. No reference counterpart (see dkv_pack_batch). */
+int dkv_pack_validate(const dkv_pack_job* jobs, int32_t n_jobs, int64_t arena_bytes,
+                      int32_t layers, int32_t heads);
 
 /* Dequantize tokens [0, n_tokens) of one layer into out[2, heads, n_tokens, 64]
  * (bf16 or fp32 by out_dtype), as q*s + a in fp32 (src/kv_quantization.py:90-92).

@@ -148,3 +148,23 @@ def test_attend_demands_workspace_when_split():
     assert need > 0
     assert lib.dkv_attend(ctypes.byref(a), None) == _lib.DKV_EINVAL
     assert 'workspace' in lib.dkv_last_error().decode()
+
+
+def test_pack_validate_checks_every_job_of_a_host_table():
+    lib = _lib.load()
+    good = [job(seg_offset=0), job(seg_offset=4096, layer=1)]
+    table = (_lib.PackJob * 2)(*good)
+    assert lib.dkv_pack_validate(ctypes.addressof(table), 2, 1 << 20, 2, 5) == 0
+    bad = (_lib.PackJob * 3)(*good, job(seg_offset=1 << 20))
+    assert lib.dkv_pack_validate(ctypes.addressof(bad), 3, 1 << 20, 2, 5) == _lib.DKV_EINVAL
+    assert 'outside' in lib.dkv_last_error().decode()
+    neg = (_lib.PackJob * 1)(job(write_tiles=1, tile_index0=-1))
+    assert lib.dkv_pack_validate(ctypes.addressof(neg), 1, 1 << 20, 2, 5) == _lib.DKV_EINVAL
+
+
+@pytest.mark.parametrize('kw', [dict(path=3), dict(path=-1), dict(precision=2)])
+def test_attend_rejects_unknown_path_or_precision(kw):
+    lib = _lib.load()
+    a = attn(**kw)
+    assert lib.dkv_attend(ctypes.byref(a), None) == _lib.DKV_EINVAL
+    assert 'path' in lib.dkv_last_error().decode()
