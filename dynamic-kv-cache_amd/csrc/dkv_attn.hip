@@ -210,9 +210,9 @@ attn_vec_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ part
 
 // Log-sum-exp merge of split partials: one thread per (row, column). The
 // splits are read CB at a time with independent loads, so a row's partials
-// stream in a few round trips instead of one per split; the running
-// (max, sum, output) is rescaled as each batch arrives.
-constexpr int CB = 16;
+// arrive in one round trip for up to CB splits (the default plan never makes
+// more than 64); the running (max, sum, output) is rescaled per batch.
+constexpr int CB = 64;
 
 __global__ void __launch_bounds__(256)
 combine_kernel(dkv_attn_args a, int splits, const float* __restrict__ part_o,

@@ -12,8 +12,7 @@
 //
 // Per unit:
 //   1. the raw K and V sub-blocks (codes + (offset, scale) pairs, or bf16 rows)
-//      are copied to LDS with one 16-byte load per thread each; the next
-//      unit's loads are issued before this unit's MFMA work;
+//      are copied to LDS with one 16-byte load per thread each;
 //   2. the 512 threads dequantize (q*s + a, fp32 multiply then add, as the
 //      reference unpack does) into a bf16 K tile [key][d] and a transposed
 //      bf16 V tile [d][key];
@@ -125,13 +124,17 @@ template <int PREC, int NBW>
 __global__ void __launch_bounds__(MF_THREADS)
 attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ part_o,
                  float2* __restrict__ part_ml) {
-  __shared__ __attribute__((aligned(16))) uint8_t raw[2][RAWP];
-  __shared__ __attribute__((aligned(16))) uint16_t k_hi[64 * KS];
-  __shared__ __attribute__((aligned(16))) uint16_t v_hi[64 * KS];
-  __shared__ __attribute__((aligned(16))) uint16_t k_lo[PREC ? 64 * KS : 8];
-  __shared__ __attribute__((aligned(16))) uint16_t v_lo[PREC ? 64 * KS : 8];
-  __shared__ __attribute__((aligned(16))) float mrg_o[MFMA_ROWS * D];
-  __shared__ float2 mrg_ml[MFMA_ROWS];
+  // LDS: two raw stages of (K, V) sub-blocks and two sets of bf16 tiles
+  // (K, V^T, and for PREC 1 their lo parts). After the last unit the same
+  // bytes hold the key-group merge (O rows, then (max, sum) pairs).
+  constexpr int NT = PREC ? 4 : 2;
+  constexpr int RAW_BYTES = 2 * 2 * RAWP;
+  constexpr int TILE_BYTES = 64 * KS * 2;
+  constexpr int SMEM = RAW_BYTES + 2 * NT * TILE_BYTES;
+  static_assert(SMEM >= MFMA_ROWS * D * 4 + MFMA_ROWS * 8, "merge buffer must fit");
+  __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
+  auto raw_buf = [&](int st, int kv) { return smem + (st * 2 + kv) * RAWP; };
+  auto tile = [&](int b, int which) { return reinterpret_cast<uint16_t*>(smem + RAW_BYTES + (b * NT + which) * TILE_BYTES); };
 
   const int split = blockIdx.x, h = blockIdx.y, rg = blockIdx.z;
   const int G = a.q_heads / a.heads;
@@ -178,24 +181,21 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ par
     l_part[nb] = 0.f;
   }
 
-  uint4 wk, wv;
-  if (u0 < u1) raw_load(a, get_unit(a, u0, h), h, wk, wv);
-
-  for (int u = u0; u < u1; ++u) {
-    const Unit un = get_unit(a, u, h);
-    *reinterpret_cast<uint4*>(raw[0] + padded(16 * t)) = wk;
-    *reinterpret_cast<uint4*>(raw[1] + padded(16 * t)) = wv;
-    __syncthreads();
-    // Dequantize into bf16 tiles: thread = (K or V, key pair kp, column block db).
+  // Dequantize a staged unit into bf16 tiles: thread = (K or V, key pair kp, column block db).
+  auto dequant = [&](const Unit& un, int st, int b) {
+    uint16_t* k_hi = tile(b, 0);
+    uint16_t* v_hi = tile(b, 1);
+    uint16_t* k_lo = tile(b, PREC ? 2 : 0);
+    uint16_t* v_lo = tile(b, PREC ? 3 : 1);
     {
       const int kv = t >> 8, kp = (t & 255) >> 3, db = t & 7;
       const int r0 = 2 * kp, r1 = r0 + 1;
       float x0[8], x1[8];
-      if (r0 < un.valid) dequant8(raw[kv], un.bits, un.rows, r0, db, x0);
+      if (r0 < un.valid) dequant8(raw_buf(st, kv), un.bits, un.rows, r0, db, x0);
       else
 #pragma unroll
         for (int i = 0; i < 8; ++i) x0[i] = 0.f;
-      if (r1 < un.valid) dequant8(raw[kv], un.bits, un.rows, r1, db, x1);
+      if (r1 < un.valid) dequant8(raw_buf(st, kv), un.bits, un.rows, r1, db, x1);
       else
 #pragma unroll
         for (int i = 0; i < 8; ++i) x1[i] = 0.f;
@@ -227,10 +227,15 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ par
         }
       }
     }
-    __syncthreads();
-    if (u + 1 < u1) raw_load(a, get_unit(a, u + 1, h), h, wk, wv);
-    if (!wave_on) continue;
+  };
 
+  // MFMA work of one dequantized unit held in tile set b.
+  auto compute = [&](const Unit& un, int b) {
+    if (!wave_on) return;
+    const uint16_t* k_hi = tile(b, 0);
+    const uint16_t* v_hi = tile(b, 1);
+    const uint16_t* k_lo = tile(b, PREC ? 2 : 0);
+    const uint16_t* v_lo = tile(b, PREC ? 3 : 1);
     const bool lo_on = PREC && un.bits != 16;
     // S^T = K Q^T over this group's 32 keys: block j holds keys 32 kg + 8 g' + 4 j + i
     // in its row 4 g' + i, so A-operand row `col` of block j is key
@@ -335,10 +340,41 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ par
             acc_o[nb][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[db].v, p_hi[nb].v, acc_o[nb][db], 0, 0, 0);
       }
     }
+  };
+
+  // Software pipeline, one barrier per unit: iteration i dequantizes unit
+  // i+1 into the other tile set, stages unit i+2's raw bytes (loaded during
+  // iteration i-1) and issues unit i+3's loads, then runs unit i's MFMA work.
+  // So one wave's dequantization overlaps another's MFMAs, and each unit's
+  // HBM latency hides behind a full iteration.
+  const int n = u1 - u0;
+  auto stage = [&](int st, const uint4& wk, const uint4& wv) {
+    *reinterpret_cast<uint4*>(raw_buf(st, 0) + padded(16 * t)) = wk;
+    *reinterpret_cast<uint4*>(raw_buf(st, 1) + padded(16 * t)) = wv;
+  };
+  uint4 wk, wv;
+  if (n > 0) {
+    raw_load(a, get_unit(a, u0, h), h, wk, wv);
+    stage(0, wk, wv);
+  }
+  if (n > 1) raw_load(a, get_unit(a, u0 + 1, h), h, wk, wv);
+  __syncthreads();
+  if (n > 0) dequant(get_unit(a, u0, h), 0, 0);
+  if (n > 1) stage(1, wk, wv);
+  if (n > 2) raw_load(a, get_unit(a, u0 + 2, h), h, wk, wv);
+  for (int i = 0; i < n; ++i) {
+    __syncthreads();
+    if (i + 1 < n) dequant(get_unit(a, u0 + i + 1, h), (i + 1) & 1, (i + 1) & 1);
+    if (i + 2 < n) {
+      stage(i & 1, wk, wv);
+      if (i + 3 < n) raw_load(a, get_unit(a, u0 + i + 3, h), h, wk, wv);
+    }
+    compute(get_unit(a, u0 + i, h), i & 1);
   }
 
-  // Merge the two key groups: group 1 parks (max, sum, O) in LDS, group 0
-  // folds it in. Lane (g, col) of block nb holds O^T rows d = 16 db + 4 g + i
+  // Merge the two key groups: group 1 parks (max, sum, O) in LDS (over the
+  // staging buffers, once every wave is past its last unit), group 0 folds it
+  // in. Lane (g, col) of block nb holds O^T rows d = 16 db + 4 g + i
   // of local row (w + 4 nb) * 16 + col.
   float lsum[NBW];
 #pragma unroll
@@ -348,6 +384,9 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ par
     l += __shfl_xor(l, 32);
     lsum[nb] = l;
   }
+  float* mrg_o = reinterpret_cast<float*>(smem);
+  float2* mrg_ml = reinterpret_cast<float2*>(smem + MFMA_ROWS * D * 4);
+  __syncthreads();
   if (kg == 1 && wave_on) {
 #pragma unroll
     for (int nb = 0; nb < NBW; ++nb) {
