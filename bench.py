@@ -32,7 +32,7 @@ def parse():
     p.add_argument('--steps', type=int, default=200)
     p.add_argument('--warmup', type=int, default=20)
     p.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
-    p.add_argument('--only', choices=['pack', 'attn', 'cand', 'all'], default='all')
+    p.add_argument('--only', choices=['pack', 'attn', 'cand', 'e2e', 'all'], default='all')
     p.add_argument('--rotate', type=int, default=48, help='distinct layers attention rotates over')
     return p.parse_args()
 
@@ -50,6 +50,18 @@ def time_launches(fn, steps, warmup):
     end.synchronize()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps  # ms per launch
+
+
+def pack_traffic():
+    """HBM bytes per pack launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes, each
+    scaled by what the counter reads for a 256 MiB copy (profiles/pack_batch_kernel_pack_volume.md)."""
+    path = os.path.join(REPO, 'profiles', 'pack_batch_kernel_traffic.json')
+    if not os.path.exists(path):
+        return None
+    t = json.load(open(path))
+    fetch = t['fetch_kib'] * t['copy_bytes'] / t['copy_fetch_kib']
+    write = t['write_kib'] * t['copy_bytes'] / t['copy_write_kib']
+    return int(fetch + write)
 
 
 def pack_bytes(bits, layers=LAYERS, heads=HEADS, tile=TILE):
@@ -189,6 +201,56 @@ def bench_candidates(bits, steps, warmup, rotate, precision='bf16'):
                 bytes=nbytes, flops=flops, lengths=lengths, hbm_frac=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS)
 
 
+def bench_e2e(frame_counts=(16, 64, 96), reps=2):
+    """random-init 32-layer decoder, 64-token synthetic frames, 4 candidates.
+
+    frames/s = frames / (ingest + candidate scoring) seconds, the reference's request definition
+    (benchmarks/gpu_evaluate.py:105) without video decode and the vision encoder.
+    """
+    import torch
+    from dkv.streaming import StreamingDecoder, build_decoder
+    from dkv.workloads import bit_schedule, candidate_lengths
+    dev = torch.device('cuda:0')
+    model = build_decoder(seed=0, device=dev)
+    dec = StreamingDecoder(model)
+    g = torch.Generator().manual_seed(0)
+    vocab = model.config.vocab_size
+    prefix = torch.randint(0, vocab, (1, 16), generator=g)
+    question = torch.randint(0, vocab, (1, 24), generator=g)
+    cands = [torch.randint(0, vocab, (1, n), generator=g) for n in candidate_lengths(0, 4)]
+    out = {}
+    for nf in frame_counts:
+        ids = torch.randint(0, vocab, (nf, 64), generator=g).to(dev)
+        with torch.inference_mode():
+            emb = model.model.get_input_embeddings()(ids)
+        frames = [emb[i:i + 1] for i in range(nf)]
+        bits = bit_schedule(nf, nf)
+        best = {}
+        for proto in ('forks', 'batched'):
+            times = []
+            for _ in range(reps + 1):  # the first request warms up kernels and GEMM selection
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                cache = dec.ingest(prefix, frames, bits)
+                if proto == 'forks':
+                    scores = dec.answer(cache, question, cands)
+                else:
+                    scores = dec.answer_batched(cache, question, cands)
+                scores.cpu()
+                torch.cuda.synchronize()
+                times.append(time.perf_counter() - t0)
+                del cache
+            best[proto] = min(times[1:])
+        out[f'frames_{nf}'] = dict(frames_per_s_forks=round(nf / best['forks'], 2),
+                                   frames_per_s_batched=round(nf / best['batched'], 2),
+                                   request_s_forks=round(best['forks'], 4),
+                                   request_s_batched=round(best['batched'], 4),
+                                   tokens=16 + 64 * nf + 24 + sum(c.shape[1] for c in cands))
+        print(f"# e2e {nf} frames: {out[f'frames_{nf}']['frames_per_s_forks']} frames/s (forks), "
+              f"{out[f'frames_{nf}']['frames_per_s_batched']} frames/s (batched)", flush=True)
+    return out
+
+
 def cpu_baselines(target_s=8.0):
     """The reference CPU path restated in torch on this host's cores (oracle; timed, not checked)."""
     import torch
@@ -267,6 +329,8 @@ def main():
                 res['candidates'][f'{prec}_{bits}bit'] = r
                 print(f"# candidates {prec} {bits}-bit: {r['us_per_batch']:.2f} us, {r['gbs']:.0f} GB/s, "
                       f"{r['tflops']:.1f} TFLOP/s", flush=True)
+    if args.only in ('e2e', 'all'):
+        res['e2e'] = bench_e2e()
     cpu = None if args.no_cpu else cpu_baselines()
     p = res.get('pack')
     line = dict(
@@ -280,7 +344,8 @@ def main():
     )
     if p:
         line['roofline'] = dict(bound='hbm', achieved=round(p['gbs'], 1), peak=HBM_PEAK_GBS,
-                                unit='GB/s', frac=round(p['gbs'] / HBM_PEAK_GBS, 4), traffic=None)
+                                unit='GB/s', frac=round(p['gbs'] / HBM_PEAK_GBS, 4), traffic=pack_traffic(),
+                                algorithmic_bytes=p['read_bytes'] + p['write_bytes'])
         line['copy_reference_gbs'] = round(res['copy']['gbs'], 1)
     if 'attention' in res:
         line['attention'] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in r.items()}
@@ -288,6 +353,8 @@ def main():
     if 'candidates' in res:
         line['candidates'] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in r.items()}
                               for k, r in res['candidates'].items()}
+    if 'e2e' in res:
+        line['e2e'] = res['e2e']
     if cpu:
         line['cpu_baseline'] = dict(value=round(cpu['pack_gbs'], 4), unit='GB/s', cores=cpu['cores'], kind='port',
                                     sample=cpu['pack_sample'],

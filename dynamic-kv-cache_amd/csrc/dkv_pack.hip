@@ -125,7 +125,7 @@ __device__ __forceinline__ void pack_wave(const dkv_pack_job& j, int kv, int hea
       const int r = 8 * i + (lane >> 3);
       if (r >= nrows) continue;
       uint8_t* dst = one_tile ? d0.payload + r * 128 : row_dst(j, kv, head, tok0 + r, arena, layers, heads).payload;
-      __builtin_nontemporal_store(w[i], reinterpret_cast<u32x4*>(dst + 16 * c));
+      *reinterpret_cast<u32x4*>(dst + 16 * c) = w[i];
     }
     return;
   }
@@ -202,7 +202,7 @@ __device__ __forceinline__ void pack_wave(const dkv_pack_job& j, int kv, int hea
   for (int i = 0; i < RB / 16; ++i) {
     const int off = 16 * (lane + 64 * i);
     if (off < bytes)
-      __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(lds + off), reinterpret_cast<u32x4*>(d0.payload + off));
+      *reinterpret_cast<u32x4*>(d0.payload + off) = *reinterpret_cast<const u32x4*>(lds + off);
   }
 }
 

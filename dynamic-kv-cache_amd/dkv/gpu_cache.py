@@ -91,6 +91,7 @@ class GPUCache(_CacheBase):
         self.cursors = [0] * layers
         self.pending_bits = 16
         self.frame_id = -1
+        self.chunk_segments = None  # default `segments` of attend() (batched continuations)
         self.online = plan is None
         self.plan = []  # (start, end, bits, row) per segment, as in the reference
         self.segments = []
@@ -184,6 +185,24 @@ class GPUCache(_CacheBase):
 
     def __len__(self):
         return self.layers
+
+    # Mask-size queries of transformers 5.x (masking_utils._preprocess_mask_arguments). The fused
+    # attention applies its own bottom-right causal mask and never reads the dense one.
+    @property
+    def is_sliding(self):
+        return [False] * self.layers
+
+    @property
+    def is_compileable(self):
+        return False
+
+    def get_query_offset(self, layer_idx=0):
+        return self.seen[layer_idx or 0]
+
+    def get_mask_sizes(self, query_length, layer_idx=0):
+        if isinstance(query_length, torch.Tensor):
+            query_length = query_length.shape[0]
+        return self.seen[layer_idx or 0] + query_length, 0
 
     def _tiles_before(self, past):
         return bisect.bisect_left(self.tile_starts, past)
@@ -332,6 +351,10 @@ class GPUCache(_CacheBase):
             raise ValueError('attend: history longer than the cache holds')
         if q.device.type != 'cuda' or k.device != q.device or v.device != q.device:
             raise ValueError('attend requires CUDA tensors on one device')
+        if segments is None:
+            segments = self.chunk_segments
+        if segments is not None and (segments[0] != 0 or segments[-1] != n):
+            raise ValueError(f'chunk segments {segments} do not cover the {n}-token chunk')
         q, k, v = self._kv_view(q), self._kv_view(k), self._kv_view(v)
         out = torch.empty((1, n, q.shape[1], self.dim), dtype=out_dtype or q.dtype, device=q.device)
         a = self.attend_args(q, k, v, layer, past, out, segments, path, splits, precision)

@@ -1,0 +1,134 @@
+"""Streaming decoder over the packed cache: frame ingestion and candidate scoring.
+
+The caller side of the packed-KV path, following the reference's StreamingModel
+(src/streaming.py:89-237) on a text decoder with synthetic frame embeddings in
+place of the vision encoder:
+
+- ingest(): one decoder forward for a text prefix, then one per 64-token frame.
+  The cache's width is selected per frame (cache.select(bits, i),
+  src/streaming.py:178), and every LlamaAttention packs its K/V and attends
+  over the packed history (install_packed_attention).
+- answer(): the reference's 'candidate' protocol (src/streaming.py:209-225).
+  For each candidate, a fork of the cache runs question + candidate tokens, and
+  the score is the mean log-likelihood of the candidate tokens.
+- answer_batched(): the same scores from one forward of the question on a fork,
+  then one forward of all candidates together. The candidates sit back to back
+  in one chunk with per-candidate positions and a block-diagonal chunk mask
+  (GPUCache.chunk_segments), so the shared history is read once per batch
+  instead of once per candidate.
+
+The model is a random-init LlamaForCausalLM. There is no checkpoint, and the
+workloads are synthetic; see dkv.workloads.decoder_config.
+"""
+import torch
+
+from .gpu_cache import GPUCache, install_packed_attention
+from .gpu_ops import install_fused_ops
+
+
+def build_decoder(layers=32, hidden=960, heads=15, kv_heads=5, intermediate=2560, vocab=49280,
+                  rope_theta=100000.0, max_positions=8192, seed=0, device='cuda', dtype=torch.bfloat16):
+    """A random-init Llama text decoder of the given shape, on `device`, in eval mode."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+    config = LlamaConfig(vocab_size=vocab, hidden_size=hidden, intermediate_size=intermediate,
+                         num_hidden_layers=layers, num_attention_heads=heads, num_key_value_heads=kv_heads,
+                         head_dim=hidden // heads, hidden_act='silu', rms_norm_eps=1e-5,
+                         max_position_embeddings=max_positions, rope_theta=rope_theta,
+                         tie_word_embeddings=True, attn_implementation='sdpa')
+    with torch.random.fork_rng(devices=[]):
+        torch.manual_seed(seed)
+        model = LlamaForCausalLM(config)
+    return model.to(device=device, dtype=dtype).eval()
+
+
+class StreamingDecoder:
+    """Frame-by-frame ingestion into a GPUCache and candidate scoring (src/streaming.py:89-237)."""
+
+    def __init__(self, model, fused_ops=True, precision='bf16'):
+        self.model = model
+        self.text = model.model
+        self.config = model.config
+        self.precision = precision
+        self.ops_state = {'enabled': fused_ops}
+        install_fused_ops(self.text, self.ops_state)
+        install_packed_attention(model)
+
+    @property
+    def device(self):
+        return self.model.lm_head.weight.device
+
+    def create_cache(self, max_tokens, **kw):
+        c = self.config
+        return GPUCache(None, layers=c.num_hidden_layers, heads=c.num_key_value_heads, dim=c.head_dim,
+                        dtype=self.model.dtype, max_tokens=max_tokens, precision=self.precision,
+                        device=self.device, **kw)
+
+    @torch.inference_mode()
+    def forward(self, cache, ids=None, embeddings=None, positions=None, logits=0):
+        """One decoder forward of a chunk. Returns fp32 logits of the last `logits` positions."""
+        if embeddings is None:
+            embeddings = self.text.get_input_embeddings()(ids.to(self.device))
+        past = cache.get_seq_length()
+        n = embeddings.shape[1]
+        if positions is None:
+            positions = torch.arange(past, past + n, device=self.device)
+        out = self.text(inputs_embeds=embeddings, past_key_values=cache, use_cache=True,
+                        position_ids=positions[None], attention_mask=None, return_dict=True)
+        if not logits:
+            return None
+        return self.model.lm_head(out.last_hidden_state[:, -int(logits):]).float()
+
+    @torch.inference_mode()
+    def ingest(self, prefix_ids, frames, bits, cache=None, qa_reserve=256):
+        """Prefix at 16 bits, then each frame embedding [1, T, hidden] at its width (src/streaming.py:168-187)."""
+        if len(frames) != len(bits):
+            raise ValueError('one bit width per frame')
+        if cache is None:
+            total = prefix_ids.shape[1] + sum(f.shape[1] for f in frames) + qa_reserve
+            cache = self.create_cache(total)
+        cache.select(16, -1)
+        self.forward(cache, ids=prefix_ids)
+        for i, (emb, b) in enumerate(zip(frames, bits)):
+            cache.select(b, i)
+            self.forward(cache, embeddings=emb)
+        cache.select(16, -1)
+        if len(set(cache.seen)) != 1:
+            raise RuntimeError('Decoder layers disagree about the cache length')
+        return cache
+
+    @staticmethod
+    def _mean_loglik(logits, targets):
+        return logits.log_softmax(-1).gather(1, targets[:, None]).mean()
+
+    @torch.inference_mode()
+    def answer(self, cache, question_ids, candidates):
+        """Mean token log-likelihood of each candidate on its own fork (src/streaming.py:209-225)."""
+        scores = []
+        for cand in candidates:
+            ids = torch.cat((question_ids, cand), dim=1).to(self.device)
+            branch = cache.fork()
+            lg = self.forward(branch, ids=ids, logits=cand.shape[1] + 1)
+            scores.append(self._mean_loglik(lg[0, :-1], cand[0].to(self.device)))
+        return torch.stack(scores)
+
+    @torch.inference_mode()
+    def answer_batched(self, cache, question_ids, candidates):
+        """The same scores with the question once and all candidates in one block-diagonal chunk."""
+        branch = cache.fork()
+        q_logits = self.forward(branch, ids=question_ids, logits=1)[0]  # predicts each candidate's first token
+        past = branch.get_seq_length()
+        ids = torch.cat(candidates, dim=1).to(self.device)
+        bounds = [0]
+        for cand in candidates:
+            bounds.append(bounds[-1] + cand.shape[1])
+        positions = torch.cat([torch.arange(past, past + c.shape[1], device=self.device) for c in candidates])
+        branch.chunk_segments = bounds
+        try:
+            lg = self.forward(branch, ids=ids, positions=positions, logits=ids.shape[1])[0]
+        finally:
+            branch.chunk_segments = None
+        scores = []
+        for i, cand in enumerate(candidates):
+            pred = torch.cat((q_logits, lg[bounds[i]:bounds[i + 1] - 1]), 0)
+            scores.append(self._mean_loglik(pred, cand[0].to(self.device)))
+        return torch.stack(scores)

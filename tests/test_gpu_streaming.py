@@ -1,0 +1,93 @@
+"""The decoder side of the path: a random-init Llama running on the packed cache.
+
+Mirrors the reference's integration checks: the packed fused path against the
+upstream DynamicCache + SDPA forward (scripts/gpu_model_smoke.py:23-24 compares
+fused and native label scores with a 0.3 bound), and candidate scoring
+(src/streaming.py:209-225).
+
+Tolerances:
+  all-16-bit packed cache (precision='fp32') vs native DynamicCache: logits max-abs <= 0.05.
+    Both run the same bf16 GEMMs; only attention differs (fp32-accurate packed kernel vs
+    torch SDPA in bf16), so the logits agree to a few bf16 ulps of their ~N(0, 1) scale.
+  batched candidate scoring vs one fork per candidate: mean log-likelihoods within 2e-2. The
+    chunk's GEMMs run at different M, which can change bf16 rounding; the scores are means
+    over 8-24 tokens of log-softmax over a 512-word vocabulary (|score| ~ 6).
+"""
+import pytest
+import torch
+
+from conftest import announce
+from dkv.streaming import StreamingDecoder, build_decoder
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(layers=2, hidden=384, heads=6, kv_heads=2, intermediate=768, vocab=512, max_positions=4096)
+
+
+def frames_for(model, n_frames, seed, tokens=64):
+    """Frame embeddings: embeddings of random token ids (the model's own input scale)."""
+    g = torch.Generator().manual_seed(seed)
+    ids = torch.randint(0, model.config.vocab_size, (n_frames, tokens), generator=g)
+    emb = model.model.get_input_embeddings()(ids.to(model.lm_head.weight.device))
+    return [emb[i:i + 1] for i in range(n_frames)]
+
+
+def native_logits(model, prefix, frames, question):
+    from transformers import DynamicCache
+    cache = DynamicCache()
+    with torch.inference_mode():
+        model.model(input_ids=prefix.cuda(), past_key_values=cache, use_cache=True)
+        for emb in frames:
+            model.model(inputs_embeds=emb, past_key_values=cache, use_cache=True)
+        out = model.model(input_ids=question.cuda(), past_key_values=cache, use_cache=True)
+        return model.lm_head(out.last_hidden_state).float()
+
+
+def test_packed_16bit_matches_native_decoder(cuda):
+    announce('streaming: 16-bit packed vs native DynamicCache, 2-layer decoder')
+    model = build_decoder(**SMALL, seed=3)
+    g = torch.Generator().manual_seed(4)
+    prefix = torch.randint(0, 512, (1, 16), generator=g)
+    question = torch.randint(0, 512, (1, 24), generator=g)
+    frames = frames_for(model, 5, seed=5)
+    ref = native_logits(model, prefix, frames, question)
+    dec = StreamingDecoder(model, precision='fp32')
+    cache = dec.ingest(prefix, frames, [16] * len(frames))
+    got = dec.forward(cache, ids=question, logits=question.shape[1])
+    torch.cuda.synchronize()
+    assert cache.get_seq_length() == 16 + 5 * 64 + 24
+    err = (got - ref).abs().max().item()
+    assert err <= 0.05, err
+
+
+def test_batched_candidates_match_sequential_forks(cuda):
+    announce('streaming: batched candidate scoring vs sequential forks')
+    model = build_decoder(**SMALL, seed=6)
+    dec = StreamingDecoder(model, precision='fp32')
+    g = torch.Generator().manual_seed(7)
+    prefix = torch.randint(0, 512, (1, 16), generator=g)
+    frames = frames_for(model, 4, seed=8)
+    cache = dec.ingest(prefix, frames, [4, 8, 16, 4])
+    question = torch.randint(0, 512, (1, 20), generator=g)
+    cands = [torch.randint(0, 512, (1, n), generator=g) for n in (9, 17, 12, 24)]
+    seen = cache.get_seq_length()
+    seq = dec.answer(cache, question, cands)
+    bat = dec.answer_batched(cache, question, cands)
+    torch.cuda.synchronize()
+    assert cache.get_seq_length() == seen  # forks never advance the base cache
+    assert torch.isfinite(seq).all() and torch.isfinite(bat).all()
+    assert (seq - bat).abs().max().item() <= 2e-2, (seq, bat)
+
+
+def test_mixed_width_ingest_tracks_the_schedule(cuda):
+    announce('streaming: mixed-width ingest accounting')
+    model = build_decoder(**SMALL, seed=9)
+    dec = StreamingDecoder(model)
+    prefix = torch.randint(0, 512, (1, 16))
+    bits = [4, 8, 16, 4, 8, 4]
+    cache = dec.ingest(prefix, frames_for(model, len(bits), seed=10), bits)
+    acct = cache.accounting()
+    assert acct['precision_token_counts'] == {4: 3 * 64, 8: 2 * 64, 16: 64 + 16}
+    assert [s.bits for s in cache.segments] == [16] + bits
+    logits = dec.forward(cache, ids=torch.randint(0, 512, (1, 8)), logits=8)
+    assert torch.isfinite(logits).all()
