@@ -32,7 +32,7 @@ def parse():
     p.add_argument('--steps', type=int, default=200)
     p.add_argument('--warmup', type=int, default=20)
     p.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
-    p.add_argument('--only', choices=['pack', 'attn', 'cand', 'e2e', 'all'], default='all')
+    p.add_argument('--only', choices=['pack', 'seg', 'attn', 'cand', 'e2e', 'all'], default='all')
     p.add_argument('--rotate', type=int, default=48, help='distinct layers attention rotates over')
     return p.parse_args()
 
@@ -102,6 +102,31 @@ def bench_pack(steps, warmup, reps=10):
     read, write = pack_bytes(vol['bits'])
     gbs = (read + write) / (ms * 1e-3) / 1e9
     return dict(ms=ms, gbs=gbs, read_bytes=read, write_bytes=write, bits=vol['bits'], steps=rounds * reps)
+
+
+def bench_segments(steps, warmup, reps=10):
+    """Export of the whole pack volume into the reference's PackedTensor layout (one launch over all
+    96 segments x 32 layers), and import of those segments into a second cache. Both are byte moves:
+    algorithmic bytes = payload + fp32 offsets/scales read once and written once."""
+    import torch
+    from dkv.gpu_cache import GPUCache, SegmentExport
+    from dkv.workloads import pack_volume
+    vol = pack_volume(seed=0, layers=LAYERS, frames=96)
+    dev = torch.device('cuda:0')
+    src = GPUCache(None, layers=LAYERS, heads=HEADS, max_tokens=96 * TILE)
+    src.append_batch(vol['k'].to(dev), vol['v'].to(dev), vol['bits'], [TILE] * 96)
+    exp = SegmentExport(src).run()
+    rounds = max(1, steps // reps)
+    ms_export = time_launches(graph_of(exp.run, reps).replay, rounds, max(1, warmup // reps)) / reps
+    dst = GPUCache(None, layers=LAYERS, heads=HEADS, max_tokens=96 * TILE)
+    _, batch = dst._import(exp.segments())
+    ms_import = time_launches(graph_of(batch.run, reps).replay, rounds, max(1, warmup // reps)) / reps
+    torch.cuda.synchronize()
+    same = bool(torch.equal(dst.arena[:dst.arena_used], src.arena[:src.arena_used]))
+    moved = 2 * exp.nbytes
+    return dict(export_us=ms_export * 1e3, export_gbs=moved / (ms_export * 1e-3) / 1e9,
+                import_us=ms_import * 1e3, import_gbs=moved / (ms_import * 1e-3) / 1e9,
+                algorithmic_bytes=moved, segments=len(exp.parts), arena_round_trip_equal=same)
 
 
 def bench_copy(steps, nbytes=256 << 20, reps=10):
@@ -313,6 +338,10 @@ def main():
         print(f"# pack: {res['pack']['ms'] * 1e3:.1f} us/launch, {res['pack']['gbs']:.0f} GB/s", flush=True)
         res['copy'] = bench_copy(args.steps)
         print(f"# copy 256 MiB: {res['copy']['ms'] * 1e3:.1f} us, {res['copy']['gbs']:.0f} GB/s", flush=True)
+    if args.only in ('seg', 'all'):
+        r = res['segments'] = bench_segments(args.steps, args.warmup)
+        print(f"# segments: export {r['export_us']:.1f} us ({r['export_gbs']:.0f} GB/s), import {r['import_us']:.1f} "
+              f"us ({r['import_gbs']:.0f} GB/s), round trip equal {r['arena_round_trip_equal']}", flush=True)
     if args.only in ('attn', 'all'):
         res['attention'] = {}
         for prec in ('bf16', 'fp32'):
@@ -353,6 +382,8 @@ def main():
     if 'candidates' in res:
         line['candidates'] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in r.items()}
                               for k, r in res['candidates'].items()}
+    if 'segments' in res:
+        line['segments'] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in res['segments'].items()}
     if 'e2e' in res:
         line['e2e'] = res['e2e']
     if cpu:

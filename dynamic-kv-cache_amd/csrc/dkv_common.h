@@ -28,6 +28,32 @@ __host__ __device__ inline int64_t slab_bytes(int rows, int bits, int layers, in
   return subblock_bytes(rows, bits) * (int64_t)layers * 2 * heads;
 }
 
+// Tile descriptors of one segment, written by the lanes of one wave.
+__device__ __forceinline__ void write_tile_descriptors(int64_t seg_offset, int seg_rows, int seg_token_start,
+                                                      int bits, int tile_index0, int layers, int heads,
+                                                      dkv_tile* tiles) {
+  const int ntiles = (seg_rows + TILE - 1) / TILE;
+  const int64_t full = slab_bytes(TILE, bits, layers, heads);
+  for (int t = threadIdx.x & 63; t < ntiles; t += 64) {
+    dkv_tile d;
+    d.offset = seg_offset + (int64_t)t * full;
+    d.token_start = seg_token_start + t * TILE;
+    const int r = seg_rows - t * TILE;
+    d.rows = (uint16_t)(r < TILE ? r : TILE);
+    d.bits = (uint8_t)bits;
+    d.reserved = 0;
+    tiles[tile_index0 + t] = d;
+  }
+}
+
+// Byte span [seg_offset, end) of a segment of seg_rows rows in the arena.
+__host__ __device__ inline int64_t segment_end(int64_t seg_offset, int seg_rows, int bits, int layers,
+                                               int heads) {
+  const int ntiles = (seg_rows + TILE - 1) / TILE;
+  return seg_offset + (int64_t)(ntiles - 1) * slab_bytes(TILE, bits, layers, heads) +
+         slab_bytes(seg_rows - (ntiles - 1) * TILE, bits, layers, heads);
+}
+
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 

@@ -206,21 +206,10 @@ __device__ __forceinline__ void pack_wave(const dkv_pack_job& j, int kv, int hea
   }
 }
 
-// Tile descriptors of the job's segment, written by the lanes of one wave.
 __device__ __forceinline__ void write_segment_tiles(const dkv_pack_job& j, int layers, int heads,
                                                     dkv_tile* tiles) {
-  const int ntiles = (j.seg_rows + TILE - 1) / TILE;
-  const int64_t full = slab_bytes(TILE, j.bits, layers, heads);
-  for (int t = threadIdx.x & 63; t < ntiles; t += 64) {
-    dkv_tile d;
-    d.offset = j.seg_offset + (int64_t)t * full;
-    d.token_start = j.seg_token_start + t * TILE;
-    const int r = j.seg_rows - t * TILE;
-    d.rows = (uint16_t)(r < TILE ? r : TILE);
-    d.bits = (uint8_t)j.bits;
-    d.reserved = 0;
-    tiles[j.tile_index0 + t] = d;
-  }
+  write_tile_descriptors(j.seg_offset, j.seg_rows, j.seg_token_start, j.bits, j.tile_index0, layers, heads,
+                         tiles);
 }
 
 // Wave index -> (kv, head, 64-token slice) of the job; the bit width is
@@ -343,9 +332,7 @@ static int check_job(const dkv_pack_job& j, int64_t arena_bytes, int layers, int
     set_error("dkv_pack: layer %d outside [0, %d) or heads %d", j.layer, layers, heads);
     return DKV_EINVAL;
   }
-  const int ntiles = (j.seg_rows + TILE - 1) / TILE;
-  const int64_t end = j.seg_offset + (int64_t)(ntiles - 1) * slab_bytes(TILE, j.bits, layers, heads) +
-                      slab_bytes(j.seg_rows - (ntiles - 1) * TILE, j.bits, layers, heads);
+  const int64_t end = segment_end(j.seg_offset, j.seg_rows, j.bits, layers, heads);
   if (j.seg_offset < 0 || (j.seg_offset & 15) || end > arena_bytes) {
     set_error("dkv_pack: segment [%lld, %lld) outside the %lld-byte arena or misaligned",
               (long long)j.seg_offset, (long long)end, (long long)arena_bytes);

@@ -48,6 +48,14 @@ class AttnArgs(ctypes.Structure):
                 ('workspace', ctypes.c_void_p), ('workspace_bytes', ctypes.c_int64)]
 
 
+class SegmentIO(ctypes.Structure):
+    _fields_ = [('payload', ctypes.c_void_p * 2), ('offsets', ctypes.c_void_p * 2), ('scales', ctypes.c_void_p * 2),
+                ('seg_offset', ctypes.c_int64), ('seg_rows', ctypes.c_int32), ('seg_token_start', ctypes.c_int32),
+                ('row0', ctypes.c_int32), ('rows', ctypes.c_int32), ('bits', ctypes.c_int32),
+                ('layer0', ctypes.c_int32), ('n_layers', ctypes.c_int32), ('tile_index0', ctypes.c_int32),
+                ('write_tiles', ctypes.c_int32)]
+
+
 assert ctypes.sizeof(Tile) == 16
 
 _lib = None
@@ -70,6 +78,15 @@ SIGNATURES = [
                                        ctypes.c_int32, ctypes.c_void_p]),
     ('dkv_attend_workspace_bytes', ctypes.c_int64, [ctypes.POINTER(AttnArgs)]),
     ('dkv_attend', ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
+    ('dkv_export', ctypes.c_int, [ctypes.POINTER(SegmentIO), ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32,
+                                  ctypes.c_int32, ctypes.c_void_p]),
+    ('dkv_import', ctypes.c_int, [ctypes.POINTER(SegmentIO), ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                  ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]),
+    ('dkv_segment_batch', ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                         ctypes.c_int32, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                         ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]),
+    ('dkv_segment_validate', ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int64,
+                                            ctypes.c_int32, ctypes.c_int32]),
 ]
 
 

@@ -16,7 +16,7 @@ import types
 import torch
 import torch.nn.functional as F
 
-from . import _lib
+from . import _lib, formats
 
 try:  # the reference subclasses transformers' DynamicCache; keep isinstance() working
     from transformers.cache_utils import DynamicCache as _CacheBase
@@ -58,10 +58,11 @@ def worst_case_arena_bytes(tokens, layers, heads):
 
 
 class _Segment:
-    __slots__ = ('start', 'rows', 'bits', 'offset', 'tile0')
+    __slots__ = ('start', 'rows', 'bits', 'offset', 'tile0', 'frame')
 
-    def __init__(self, start, rows, bits, offset, tile0):
+    def __init__(self, start, rows, bits, offset, tile0, frame=-1):
         self.start, self.rows, self.bits, self.offset, self.tile0 = start, rows, bits, offset, tile0
+        self.frame = frame  # frame id of the select() that opened it (the segment descriptor's frame)
 
     @property
     def end(self):
@@ -120,14 +121,14 @@ class GPUCache(_CacheBase):
                 self._open_segment(self.segments[-1].end if self.segments else 0, n, bits)
 
     # -- bookkeeping -------------------------------------------------------
-    def _open_segment(self, start, n, bits):
+    def _open_segment(self, start, n, bits, frame=-1):
         need = segment_bytes(n, bits, self.layers, self.heads)
         if self.arena_used + need > self.arena_bytes:
             self._grow(self.arena_used + need)
         tile0 = len(self.tile_starts)
         if tile0 + (n + TILE - 1) // TILE > self.tiles.shape[0]:
             raise ValueError('GPU context limit exceeded')
-        seg = _Segment(start, n, bits, self.arena_used, tile0)
+        seg = _Segment(start, n, bits, self.arena_used, tile0, frame)
         self.segments.append(seg)
         self.tile_starts.extend(range(start, start + n, TILE))
         self.plan.append((start, start + n, bits, self.host_counts[bits]))
@@ -229,7 +230,7 @@ class GPUCache(_CacheBase):
         write_tiles = 0
         if self.online:
             if layer == 0:
-                self._open_segment(past, n, self.pending_bits)
+                self._open_segment(past, n, self.pending_bits, self.frame_id)
                 write_tiles = 1
             seg = self.segments[-1] if self.segments else None
         else:
@@ -240,6 +241,7 @@ class GPUCache(_CacheBase):
             seg = self.segments[cursor] if cursor < len(self.segments) else None
             if seg is not None and layer == 0 and past == seg.start:
                 write_tiles = 1
+                seg.frame = self.frame_id
         if seg is None or past + n > seg.end or seg.bits != self.pending_bits:
             raise ValueError(f'Cache append does not match plan at token {past}, length {n}, bits {self.pending_bits}')
         if n:
@@ -274,7 +276,7 @@ class GPUCache(_CacheBase):
         start = past
         for b, n in zip(bits, lengths):
             if self.online:
-                seg = self._open_segment(start, n, b)
+                seg = self._open_segment(start, n, b, self.frame_id)
             else:
                 seg = next((s for s in self.segments if s.start <= start < s.end), None)
                 if seg is None or start + n > seg.end or seg.bits != b:
@@ -421,6 +423,182 @@ class GPUCache(_CacheBase):
                     precision_pool_capacities=self.caps,
                     used_tokens=n, precision_token_counts=used,
                     arena_used_bytes=self.arena_used)
+
+
+    # -- the reference's serialized formats (src/kv_quantization.py:12-77, src/cache_manager.py:9-58) --
+    def _layer_range(self, layers):
+        layers = list(range(self.layers)) if layers is None else list(layers)
+        if not layers or layers != list(range(layers[0], layers[0] + len(layers))) or layers[0] < 0 \
+                or layers[-1] >= self.layers:
+            raise ValueError(f'layers must be a nonempty ascending run of [0, {self.layers})')
+        return layers
+
+    def export_segments(self, layers=None, device=None):
+        """The cache as src/cache_manager.py's MixedPrecisionCache would hold it: {layer: [Segment]}.
+
+        Every segment's key and value become PackedTensors with the bytes
+        src/kv_quantization.py:pack produces for that [1, heads, rows, 64] tensor (payload,
+        fp32 scales and offsets, 64-byte header) and a 32-byte descriptor
+        (layer, frame, start, end, bits). One byte-moving launch for all segments; nothing
+        is requantized. `layers` (default all) must be consecutive and at the same length.
+        The tensors stay on the cache's device unless `device` names another.
+        """
+        return SegmentExport(self, layers).run().segments(device)
+
+    def import_segments(self, segments):
+        """Appends {layer: [Segment]} (the MixedPrecisionCache layout) to every layer; returns the old length.
+
+        Segment i of every layer must describe the same tokens, frame and width, starting at the
+        cache's current length, and hold PackedTensors of [1, heads, rows, 64] tensors with group
+        size 64 (16-bit ones in bf16). Their payload, offsets and scales are copied into the arena
+        unchanged (one launch), so attending over them equals attending over the same tokens
+        packed by append().
+        """
+        return self._import(segments)[0]
+
+    def _import(self, segments):
+        """import_segments(), also returning the SegmentBatch that ran (None if nothing moved)."""
+        if sorted(segments) != list(range(self.layers)):
+            raise ValueError('import_segments needs the segments of every layer')
+        counts = {len(v) for v in segments.values()}
+        if len(counts) != 1:
+            raise ValueError('import_segments: layers hold different numbers of segments')
+        if len(set(self.seen)) != 1:
+            raise ValueError('import_segments: every layer must be at the same length')
+        past = self.seen[0]
+        entries, end = [], past
+        for i in range(counts.pop()):
+            fields = [formats.descriptor_fields(segments[l][i].descriptor) for l in range(self.layers)]
+            layer0, frame, start, stop, bits = fields[0]
+            for l, f in enumerate(fields):
+                if f[0] != l:
+                    raise ValueError(f'segment {i} of layer {l} is labelled layer {f[0]}')
+                if f[1:] != (frame, start, stop, bits):
+                    raise ValueError(f'layers disagree about segment {i}: {f[1:]} vs {(frame, start, stop, bits)}')
+            if bits not in BITS or start != end or stop <= start:
+                raise ValueError(f'segment {i} covers [{start}, {stop}) at {bits} bits; expected to start at {end}')
+            for l in range(self.layers):
+                formats.check_packed(segments[l][i].key, bits, self.heads, stop - start)
+                formats.check_packed(segments[l][i].value, bits, self.heads, stop - start)
+            entries.append((i, frame, start, stop - start, bits))
+            end = stop
+        if end > self.capacity:
+            raise ValueError('GPU context limit exceeded')
+        ios, keep, max_rows = [], [], 1
+        for i, frame, start, rows, bits in entries:
+            if self.online:
+                seg = self._open_segment(start, rows, bits, frame)
+            else:
+                seg = next((s for s in self.segments if s.start <= start < s.end), None)
+                if seg is None or start + rows > seg.end or seg.bits != bits:
+                    raise ValueError(f'Cache append does not match plan at token {start}, length {rows}, bits {bits}')
+            layer_segs = [segments[l][i] for l in range(self.layers)]
+            pay = torch.stack([torch.stack([s.key.payload for s in layer_segs]),
+                               torch.stack([s.value.payload for s in layer_segs])]).to(self.device)
+            io = _lib.SegmentIO()
+            if bits < 16:
+                meta = torch.stack([torch.stack([torch.stack([getattr(s, kv).offsets for s in layer_segs]),
+                                                 torch.stack([getattr(s, kv).scales for s in layer_segs])])
+                                    for kv in ('key', 'value')]).to(self.device)
+                keep.append(meta)
+                for kv in range(2):
+                    io.offsets[kv], io.scales[kv] = meta[kv, 0].data_ptr(), meta[kv, 1].data_ptr()
+            keep.append(pay)
+            for kv in range(2):
+                io.payload[kv] = pay[kv].data_ptr()
+            io.seg_offset, io.seg_rows, io.seg_token_start = seg.offset, seg.rows, seg.start
+            io.row0, io.rows, io.bits, io.layer0, io.n_layers = start - seg.start, rows, bits, 0, self.layers
+            io.tile_index0, io.write_tiles = seg.tile0, int(start == seg.start)
+            if start == seg.start:
+                seg.frame = frame
+            ios.append(io)
+        batch = SegmentBatch(self, ios, 1, keep=keep) if ios else None
+        if batch is not None:
+            batch.run()
+        self.seen = [end] * self.layers
+        return past, batch
+
+
+class SegmentExport:
+    """The export launch of a cache's filled segments and the buffers it fills; run() relaunches it."""
+
+    def __init__(self, cache, layers=None):
+        layers = cache._layer_range(layers)
+        seen = {cache.seen[l] for l in layers}
+        if len(seen) != 1:
+            raise ValueError('export_segments: the exported layers differ in length')
+        n, nl, heads = seen.pop(), len(layers), cache.heads
+        self.cache, self.layers, self.parts, self.nbytes = cache, layers, [], 0
+        ios = []
+        for seg in cache.segments:
+            rows = min(n, seg.end) - seg.start
+            if rows <= 0:
+                break
+            rb = formats.row_bytes(seg.bits)
+            pay = torch.empty((2, nl, heads, rows, rb), dtype=torch.uint8, device=cache.device)
+            meta = (torch.empty((2, 2, nl, heads, rows), dtype=torch.float32, device=cache.device)
+                    if seg.bits < 16 else None)
+            io = _lib.SegmentIO()
+            for kv in range(2):
+                io.payload[kv] = pay[kv].data_ptr()
+                if meta is not None:
+                    io.offsets[kv], io.scales[kv] = meta[kv, 0].data_ptr(), meta[kv, 1].data_ptr()
+            io.seg_offset, io.seg_rows, io.seg_token_start = seg.offset, seg.rows, seg.start
+            io.row0, io.rows, io.bits, io.layer0, io.n_layers = 0, rows, seg.bits, layers[0], nl
+            ios.append(io)
+            self.parts.append((seg, rows, pay, meta))
+            self.nbytes += pay.numel() + (meta.numel() * 4 if meta is not None else 0)
+        self.batch = SegmentBatch(cache, ios, 0) if ios else None
+
+    def run(self):
+        if self.batch is not None:
+            self.batch.run()
+        return self
+
+    def segments(self, device=None):
+        """{layer: [Segment]} over the buffers (moved to `device` if given)."""
+        c = self.cache
+        out = {l: [] for l in self.layers}
+        for seg, rows, pay, meta in self.parts:
+            if device is not None:
+                pay = pay.to(device)
+                meta = meta.to(device) if meta is not None else None
+            empty = torch.empty(0, dtype=torch.float32, device=pay.device)
+            # 16-bit rows are stored as bf16; 4/8-bit headers carry the dtype the cache was given
+            hdr_dtype = torch.bfloat16 if seg.bits == 16 else c.dtype
+            for i, l in enumerate(self.layers):
+                packed = []
+                for kv in range(2):
+                    hdr = formats.header(seg.bits, c.heads, rows, hdr_dtype)
+                    if meta is None:
+                        packed.append(formats.PackedTensor(pay[kv, i].flatten(), empty, empty, hdr))
+                    else:
+                        packed.append(formats.PackedTensor(pay[kv, i].flatten(), meta[kv, 1, i].flatten(),
+                                                           meta[kv, 0, i].flatten(), hdr))
+                desc = formats.descriptor(l, seg.frame, seg.start, seg.start + rows, seg.bits)
+                out[l].append(formats.Segment(packed[0], packed[1], desc))
+        return out
+
+
+class SegmentBatch:
+    """A device table for dkv_segment_batch (direction 0 exports, 1 imports); run() relaunches it."""
+
+    def __init__(self, cache, ios, direction, keep=()):
+        self.cache, self.direction, self.n, self._keep = cache, direction, len(ios), keep
+        self.max_rows = max(io.seg_rows for io in ios)
+        self.max_layers = max(io.n_layers for io in ios)
+        table = (_lib.SegmentIO * len(ios))(*ios)
+        # the kernel trusts the device table: check the host copy against the arena first
+        _lib.check(_lib.load().dkv_segment_validate(ctypes.addressof(table), len(ios), direction, cache.arena_bytes,
+                                                    cache.layers, cache.heads), 'dkv_segment_validate')
+        self.table = torch.frombuffer(bytearray(bytes(table)), dtype=torch.uint8).to(cache.device)
+
+    def run(self):
+        c = self.cache
+        _lib.check(_lib.load().dkv_segment_batch(self.table.data_ptr(), self.n, self.max_rows, self.max_layers,
+                                                 self.direction, c.arena.data_ptr(), c.arena_bytes,
+                                                 c.tiles.data_ptr(), c.layers, c.heads,
+                                                 _lib.stream_handle(c.device)), 'dkv_segment_batch')
 
 
 class PackBatch:

@@ -96,6 +96,32 @@ typedef struct dkv_attn_args {
   int64_t workspace_bytes;
 } dkv_attn_args;
 
+/* One segment of the arena in the reference's CPU-cache layout: what
+ * src/kv_quantization.py:41-77 (pack) produces for the [1, heads, rows, 64]
+ * K or V tensor of one layer. For layer l = layer0 + i (i < n_layers) and
+ * kv 0 = K, 1 = V:
+ *   payload[kv] + ((i*heads + h)*rows + r)*row_bytes   row r of head h
+ *       (row_bytes 32 / 64 / 128 for 4 / 8 / 16 bits: the PackedTensor payload)
+ *   offsets[kv][(i*heads + h)*rows + r], scales[kv][...]   fp32 (4/8-bit only;
+ *       the PackedTensor offsets and scales, one group per row)
+ * Segment rows [row0, row0 + rows) move, as buffer rows [0, rows); the arena
+ * geometry comes from seg_rows. The segment descriptor of src/cache_manager.py:9
+ * ('<iiqqB7x': layer, frame, start, end, bits) stays on the host. */
+typedef struct dkv_segment_io {
+  void* payload[2];
+  float* offsets[2];       /* NULL for 16-bit */
+  float* scales[2];        /* NULL for 16-bit */
+  int64_t seg_offset;      /* byte offset of the segment in the arena */
+  int32_t seg_rows;        /* tokens the segment can hold */
+  int32_t seg_token_start; /* logical index of the segment's first token */
+  int32_t row0;            /* first segment row moved */
+  int32_t rows;            /* rows moved */
+  int32_t bits;            /* 4, 8 or 16 */
+  int32_t layer0, n_layers;
+  int32_t tile_index0;     /* import: table index of the segment's first tile */
+  int32_t write_tiles;     /* import: nonzero also writes the segment's tile descriptors */
+} dkv_segment_io;
+
 /* Library version: DKV_ABI_VERSION. */
 int dkv_version(void);
 
@@ -145,6 +171,35 @@ int64_t dkv_attend_workspace_bytes(const dkv_attn_args* args);
  * Output rows are written to out + m*out_tok_stride + qh*out_head_stride
  * (elements), the reference's [1, nq, q_heads, 64] layout when contiguous. */
 int dkv_attend(const dkv_attn_args* args, void* stream);
+
+/* Copy one segment out of the arena into the reference's PackedTensor buffers
+ * (src/kv_quantization.py:12-77). Together with the host-side 64-byte header
+ * and the 32-byte segment descriptor (src/cache_manager.py:9,53-58), this
+ * yields the segments src/cache_manager.py's MixedPrecisionCache.update
+ * stores, byte for byte. A plain byte move: nothing is requantized. */
+int dkv_export(const dkv_segment_io* io, const void* arena, int64_t arena_bytes,
+               int32_t layers, int32_t heads, void* stream);
+
+/* The inverse of dkv_export: writes PackedTensor payloads, offsets and scales
+ * into a segment of the arena (and its tile descriptors when write_tiles), so
+ * that segments packed elsewhere by src/kv_quantization.py:pack can be attended
+ * without being requantized. */
+int dkv_import(const dkv_segment_io* io, void* arena, int64_t arena_bytes, dkv_tile* tiles,
+               int32_t layers, int32_t heads, void* stream);
+
+/* Batched dkv_export / dkv_import over a DEVICE array of n_ios segments, one
+ * launch (validate the host copy with dkv_segment_validate first). max_rows
+ * bounds every segment's seg_rows and max_layers its n_layers. direction 0
+ * exports, 1 imports. No reference counterpart: the whole-cache form of the
+ * two calls above. */
+int dkv_segment_batch(const dkv_segment_io* ios, int32_t n_ios, int32_t max_rows, int32_t max_layers,
+                      int32_t direction, void* arena, int64_t arena_bytes, dkv_tile* tiles,
+                      int32_t layers, int32_t heads, void* stream);
+
+/* Checks a HOST copy of a dkv_segment_io table (what dkv_export and dkv_import
+ * check for one segment). No reference counterpart (see dkv_segment_batch). */
+int dkv_segment_validate(const dkv_segment_io* ios, int32_t n_ios, int32_t direction,
+                         int64_t arena_bytes, int32_t layers, int32_t heads);
 
 #ifdef __cplusplus
 }

@@ -38,6 +38,7 @@ int main(void) {
   printf("dkv_tile size %zu\n", sizeof(dkv_tile));
   printf("dkv_pack_job size %zu\n", sizeof(dkv_pack_job));
   printf("dkv_attn_args size %zu\n", sizeof(dkv_attn_args));
+  printf("dkv_segment_io size %zu\n", sizeof(dkv_segment_io));
   %FIELDS%
   return 0;
 }
@@ -45,7 +46,7 @@ int main(void) {
 
 
 @pytest.mark.parametrize('cls,cname', [(_lib.Tile, 'dkv_tile'), (_lib.PackJob, 'dkv_pack_job'),
-                                       (_lib.AttnArgs, 'dkv_attn_args')])
+                                       (_lib.AttnArgs, 'dkv_attn_args'), (_lib.SegmentIO, 'dkv_segment_io')])
 def test_struct_layout_matches_header(tmp_path, cls, cname):
     fields = '\n'.join(f'F({cname}, {f})' for f, _ in cls._fields_)
     src = tmp_path / 'probe.c'
@@ -168,3 +169,52 @@ def test_attend_rejects_unknown_path_or_precision(kw):
     a = attn(**kw)
     assert lib.dkv_attend(ctypes.byref(a), None) == _lib.DKV_EINVAL
     assert 'path' in lib.dkv_last_error().decode()
+
+
+def seg_io(**kw):
+    s = _lib.SegmentIO()
+    s.payload[0], s.payload[1] = 4096, 8192
+    s.offsets[0], s.offsets[1], s.scales[0], s.scales[1] = 4096, 4100, 4104, 4108
+    s.seg_offset, s.seg_rows, s.seg_token_start, s.row0, s.rows, s.bits = 0, 64, 0, 0, 64, 4
+    s.layer0, s.n_layers, s.tile_index0, s.write_tiles = 0, 2, 0, 0
+    for k, v in kw.items():
+        setattr(s, k, v)
+    return s
+
+
+@pytest.mark.parametrize('kw,msg', [
+    (dict(bits=2), 'bits'),
+    (dict(n_layers=3), 'layers'),
+    (dict(layer0=-1), 'layers'),
+    (dict(row0=10, rows=60), 'outside a segment'),
+    (dict(seg_offset=1 << 20), 'outside'),
+    (dict(seg_offset=24), 'misaligned'),
+    (dict(offsets=(ctypes.c_void_p * 2)(0, 0)), 'offset and scale'),
+])
+def test_segment_io_rejects_bad_segments_without_touching_the_device(kw, msg):
+    lib = _lib.load()
+    s = seg_io(**kw)
+    assert lib.dkv_export(ctypes.byref(s), ctypes.c_void_p(4096), 1 << 20, 2, 5, None) == _lib.DKV_EINVAL
+    assert msg in lib.dkv_last_error().decode()
+    assert lib.dkv_import(ctypes.byref(s), ctypes.c_void_p(4096), 1 << 20, ctypes.c_void_p(4096), 2, 5,
+                          None) == _lib.DKV_EINVAL
+    table = (_lib.SegmentIO * 2)(seg_io(), s)
+    assert lib.dkv_segment_validate(ctypes.addressof(table), 2, 0, 1 << 20, 2, 5) == _lib.DKV_EINVAL
+
+
+def test_segment_io_payload_alignment_and_tile_table():
+    lib = _lib.load()
+    s = seg_io()
+    s.payload[1] = 8200
+    assert lib.dkv_export(ctypes.byref(s), ctypes.c_void_p(4096), 1 << 20, 2, 5, None) == _lib.DKV_EINVAL
+    assert '16-byte' in lib.dkv_last_error().decode()
+    t = seg_io(write_tiles=1)
+    assert lib.dkv_import(ctypes.byref(t), ctypes.c_void_p(4096), 1 << 20, None, 2, 5, None) == _lib.DKV_EINVAL
+    assert 'tile table' in lib.dkv_last_error().decode()
+    sixteen = seg_io(bits=16, offsets=(ctypes.c_void_p * 2)(0, 0), scales=(ctypes.c_void_p * 2)(0, 0))
+    table = (_lib.SegmentIO * 2)(seg_io(), sixteen)
+    assert lib.dkv_segment_validate(ctypes.addressof(table), 2, 1, 1 << 20, 2, 5) == 0
+    neg = (_lib.SegmentIO * 1)(seg_io(write_tiles=1, tile_index0=-1))
+    assert lib.dkv_segment_validate(ctypes.addressof(neg), 1, 1, 1 << 20, 2, 5) == _lib.DKV_EINVAL
+    assert lib.dkv_segment_batch(ctypes.addressof(table), 2, 64, 2, 2, ctypes.c_void_p(4096), 1 << 20, None, 2, 5,
+                                 None) == _lib.DKV_EINVAL
