@@ -208,51 +208,50 @@ attn_vec_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ part
   }
 }
 
-// Log-sum-exp merge of split partials: one thread per (row, column). The
-// splits are read CB at a time with independent loads, so a row's partials
-// arrive in one round trip for up to CB splits (the default plan never makes
-// more than 64); the running (max, sum, output) is rescaled per batch.
-constexpr int CB = 64;
-
+// Log-sum-exp merge of split partials: one wave per query row, lane d owns
+// output column d. The row's split states are read 64 at a time, lane s
+// holding split s: its scale factor 2^(m_s - M) is computed once, on that lane,
+// and every lane takes it with readlane while it accumulates its column, so a
+// row costs one exp per split instead of one per split and column.
 __global__ void __launch_bounds__(256)
 combine_kernel(dkv_attn_args a, int splits, const float* __restrict__ part_o,
                const float2* __restrict__ part_ml) {
   const int h = blockIdx.y;
   const int G = a.q_heads / a.heads;
   const int R = G * a.nq;
-  const int idx = blockIdx.x * 256 + threadIdx.x;
-  const int r = idx >> 6, d = idx & 63;
+  const int r = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
   if (r >= R) return;
   const int64_t base = (int64_t)h * splits * R + r;
   float M = -INFINITY, L = 0.f, O = 0.f;
-  for (int s0 = 0; s0 < splits; s0 += CB) {
-    float2 ml[CB];
-    float o[CB];
+  for (int s0 = 0; s0 < splits; s0 += 64) {
+    const int cnt = min(64, splits - s0);
+    const float2 ml = lane < cnt ? part_ml[base + (int64_t)(s0 + lane) * R] : make_float2(-INFINITY, 0.f);
+    float bm = ml.x;
 #pragma unroll
-    for (int i = 0; i < CB; ++i) {
-      const int s = s0 + i;
-      ml[i] = s < splits ? part_ml[base + (int64_t)s * R] : make_float2(-INFINITY, 0.f);
-      o[i] = s < splits ? part_o[(base + (int64_t)s * R) * D + d] : 0.f;
-    }
-    float bm = M;
+    for (int o = 32; o > 0; o >>= 1) bm = fmaxf(bm, __shfl_xor(bm, o));
+    bm = fmaxf(bm, M);
+    if (bm == -INFINITY) continue;  // wave-uniform: every split so far saw no visible key
+    const float f = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - bm);
+    float lsum = ml.y * f;
 #pragma unroll
-    for (int i = 0; i < CB; ++i) bm = fmaxf(bm, ml[i].x);
-    if (bm == -INFINITY) continue;
-    const float f0 = exp2f(M - bm);  // 0 when M is still -inf
-    L *= f0;
+    for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o);
+    const float f0 = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - bm);
+    L = fmaf(L, f0, lsum);
     O *= f0;
+    // All of the chunk's loads are issued before the first use.
+    const float* po = part_o + (base + (int64_t)s0 * R) * D + lane;
+    float o[64];
 #pragma unroll
-    for (int i = 0; i < CB; ++i) {
-      if (ml[i].x == -INFINITY) continue;
-      const float f = exp2f(ml[i].x - bm);
-      L = fmaf(ml[i].y, f, L);
-      O = fmaf(o[i], f, O);
-    }
+    for (int i = 0; i < 64; ++i) o[i] = i < cnt ? po[(int64_t)i * R * D] : 0.f;
+#pragma unroll
+    for (int i = 0; i < 64; ++i)
+      O = fmaf(o[i], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), i)), O);
     M = bm;
   }
   const float out = O / L;
   const int g = r / a.nq, m = r - g * a.nq;
-  const int64_t off = (int64_t)m * a.out_tok_stride + (int64_t)(h * G + g) * a.out_head_stride + d;
+  const int64_t off = (int64_t)m * a.out_tok_stride + (int64_t)(h * G + g) * a.out_head_stride + lane;
   if (a.out_dtype == 1) static_cast<float*>(a.out)[off] = out;
   else static_cast<uint16_t*>(a.out)[off] = (uint16_t)f32_to_bf16_rne(out);
 }
@@ -390,8 +389,8 @@ int dkv_attend(const dkv_attn_args* args, void* stream) {
   if (rc) return rc;
   if (p.splits > 1) {
     const int R = (a.q_heads / a.heads) * a.nq;
-    hipLaunchKernelGGL(combine_kernel, dim3((R * D + 255) / 256, a.heads), dim3(256), 0, s, a, p.splits,
-                       part_o, part_ml);
+    hipLaunchKernelGGL(combine_kernel, dim3((R + 3) / 4, a.heads), dim3(256), 0, s, a, p.splits, part_o,
+                       part_ml);
   }
   return (int)hipGetLastError();
 }

@@ -13,9 +13,10 @@
 // Per unit:
 //   1. the raw K and V sub-blocks (codes + (offset, scale) pairs, or bf16 rows)
 //      are copied to LDS with one 16-byte load per thread each;
-//   2. the 512 threads dequantize (q*s + a, fp32 multiply then add, as the
-//      reference unpack does) into a bf16 K tile [key][d] and a transposed
-//      bf16 V tile [d][key];
+//   2. the 512 threads dequantize (q*s + a as one fused multiply-add; the
+//      reference's Triton expression, src/gpu_kernels.py:67-68, is open to the
+//      same contraction under Triton's default fp fusion) into a bf16 K tile
+//      [key][d] and a transposed bf16 V tile [d][key];
 //   3. each wave computes S^T = K Q^T for its blocks (keys on the MFMA M axis,
 //      queries on N), runs the online softmax per query column in registers,
 //      and accumulates O^T = V^T P^T with P^T taken straight from the S^T
@@ -48,6 +49,8 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 constexpr int MF_THREADS = 512;
 constexpr int KS = 72;       // LDS row stride, in bf16 elements, of the K and V^T tiles
 constexpr int RAWP = 9216;   // padded raw bytes of one sub-block (64 rows x 128 B + 16 B per 128 B)
+constexpr int MRG_STRIDE = D + 4;  // fp32 row stride of the key-group merge: 16 query rows of one
+                                   // store land on different banks
 
 union Pack8 {
   bf16x8 v;
@@ -61,20 +64,38 @@ __device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
 __device__ __forceinline__ float bf16_lo_f(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi_f(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+// Max / sum over the four lane groups g = lane / 16 that hold one query
+// column (lanes col, col + 16, col + 32, col + 48), with the gfx950 lane swaps
+// (VALU, no LDS round trip): after permlane32_swap the pair is (x[l mod 32],
+// x[l mod 32 + 32]), after permlane16_swap (x[row 2k], x[row 2k + 1]).
+__device__ __forceinline__ float group_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+__device__ __forceinline__ float group_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
+// The running max of a wave moves only when some column's max grows by more
+// than this (log2 units); until then p = 2^(x - m) stays below 2^8 and the
+// accumulators need no rescaling. Precision 0 keeps the reference's exact
+// running max (p is rounded to bf16 relative to it, src/gpu_kernels.py:98-102),
+// so it only skips the rescale when no column's max grew at all.
+template <int PREC>
+constexpr float rescale_log2() { return PREC ? 8.f : 0.f; }
+
 // Raw sub-blocks sit in LDS with 16 bytes of padding after every 128 bytes,
 // which spreads the rows a dequantizing wave reads over all banks.
 __device__ __forceinline__ int padded(int off) { return off + ((off >> 7) << 4); }
 
-// 8 fp32 values of row r, columns [8*db, 8*db + 8), from a raw sub-block in LDS.
+// 8 fp32 values q*s + a of row r, columns [8*db, 8*db + 8), of a 4/8-bit raw
+// sub-block in LDS (one fused multiply-add, the more accurate of the two roundings).
 __device__ __forceinline__ void dequant8(const uint8_t* raw, int bits, int rows, int r, int db, float* x) {
-  if (bits == 16) {
-    const uint4 w = *reinterpret_cast<const uint4*>(raw + padded(r * 128 + db * 16));
-    x[0] = bf16_lo_f(w.x); x[1] = bf16_hi_f(w.x);
-    x[2] = bf16_lo_f(w.y); x[3] = bf16_hi_f(w.y);
-    x[4] = bf16_lo_f(w.z); x[5] = bf16_hi_f(w.z);
-    x[6] = bf16_lo_f(w.w); x[7] = bf16_hi_f(w.w);
-    return;
-  }
   const float2 as = *reinterpret_cast<const float2*>(raw + padded(rows * (int)row_bytes(bits) + 8 * r));
   float q[8];
   if (bits == 4) {
@@ -94,7 +115,12 @@ __device__ __forceinline__ void dequant8(const uint8_t* raw, int bits, int rows,
     }
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) x[i] = __fadd_rn(__fmul_rn(q[i], as.y), as.x);
+  for (int i = 0; i < 8; ++i) x[i] = __fmaf_rn(q[i], as.y, as.x);
+}
+
+// Row r, columns [8*db, 8*db + 8), of a bf16 raw sub-block (16-bit tiles and chunk pieces).
+__device__ __forceinline__ uint4 bf16_row8(const uint8_t* raw, int r, int db) {
+  return *reinterpret_cast<const uint4*>(raw + padded(r * 128 + db * 16));
 }
 
 // One 16-byte piece of K (threads 0..511 -> pieces 0..511) and one of V.
@@ -116,6 +142,30 @@ __device__ __forceinline__ void raw_load(const dkv_attn_args& a, const Unit& un,
   }
 }
 
+// Unit u = u0 + rel of a workgroup's range. The first 64 history tiles of the
+// range come from `win`, the descriptors every wave loaded with one vector load
+// at kernel start (lane i holds unit u0 + i), so the unit walk never waits on a
+// scalar load; later tiles fall back to reading the table.
+__device__ __forceinline__ Unit unit_at(const dkv_attn_args& a, int u, int rel, int h, const uint4& win) {
+  if (u >= a.n_tiles || rel >= 64) return get_unit(a, u, h);
+  Unit un;
+  const int64_t off = (int64_t)((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)win.y, rel) << 32 |
+                                (uint32_t)__builtin_amdgcn_readlane((int)win.x, rel));
+  const int tok = __builtin_amdgcn_readlane((int)win.z, rel);
+  const uint32_t w3 = (uint32_t)__builtin_amdgcn_readlane((int)win.w, rel);
+  const int rows = (int)(w3 & 0xffffu), bits = (int)((w3 >> 16) & 0xffu);
+  un.chunk = false;
+  un.first = tok;
+  un.valid = min(rows, a.past - tok);
+  un.bits = bits;
+  un.rows = rows;
+  const int64_t sb = subblock_bytes(rows, bits);
+  const uint8_t* base = static_cast<const uint8_t*>(a.arena) + off;
+  un.ksub = base + ((int64_t)(a.layer * 2 + 0) * a.heads + h) * sb;
+  un.vsub = base + ((int64_t)(a.layer * 2 + 1) * a.heads + h) * sb;
+  return un;
+}
+
 // NBW = 16-row query blocks each wave computes (1..3). A wave whose first
 // block is past the last row skips the MFMA work (a scalar branch); other
 // waves compute all NBW blocks, those past the last row on zero queries, and
@@ -131,7 +181,7 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ par
   constexpr int RAW_BYTES = 2 * 2 * RAWP;
   constexpr int TILE_BYTES = 64 * KS * 2;
   constexpr int SMEM = RAW_BYTES + 2 * NT * TILE_BYTES;
-  static_assert(SMEM >= MFMA_ROWS * D * 4 + MFMA_ROWS * 8, "merge buffer must fit");
+  static_assert(SMEM >= MFMA_ROWS * MRG_STRIDE * 4 + MFMA_ROWS * 8, "merge buffer must fit");
   __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
   auto raw_buf = [&](int st, int kv) { return smem + (st * 2 + kv) * RAWP; };
   auto tile = [&](int b, int which) { return reinterpret_cast<uint16_t*>(smem + RAW_BYTES + (b * NT + which) * TILE_BYTES); };
@@ -181,50 +231,75 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ par
     l_part[nb] = 0.f;
   }
 
-  // Dequantize a staged unit into bf16 tiles: thread = (K or V, key pair kp, column block db).
+  // Dequantize a staged unit into bf16 tiles. Threads 0..255 build K (thread =
+  // key pair kp, column block db, db fastest: 16-byte row stores), threads
+  // 256..511 build V^T (kp fastest, so the 4-byte stores of one instruction
+  // cover 32 consecutive words of a V^T row). bf16 rows (16-bit tiles, chunk
+  // pieces) are copied or byte-permuted without a float round trip.
   auto dequant = [&](const Unit& un, int st, int b) {
-    uint16_t* k_hi = tile(b, 0);
-    uint16_t* v_hi = tile(b, 1);
-    uint16_t* k_lo = tile(b, PREC ? 2 : 0);
-    uint16_t* v_lo = tile(b, PREC ? 3 : 1);
-    {
-      const int kv = t >> 8, kp = (t & 255) >> 3, db = t & 7;
-      const int r0 = 2 * kp, r1 = r0 + 1;
-      float x0[8], x1[8];
-      if (r0 < un.valid) dequant8(raw_buf(st, kv), un.bits, un.rows, r0, db, x0);
-      else
-#pragma unroll
-        for (int i = 0; i < 8; ++i) x0[i] = 0.f;
-      if (r1 < un.valid) dequant8(raw_buf(st, kv), un.bits, un.rows, r1, db, x1);
-      else
-#pragma unroll
-        for (int i = 0; i < 8; ++i) x1[i] = 0.f;
-      if (kv == 0) {
-        uint4 h0, h1;
-        h0 = make_uint4(pk_bf16(x0[0], x0[1]), pk_bf16(x0[2], x0[3]), pk_bf16(x0[4], x0[5]), pk_bf16(x0[6], x0[7]));
-        h1 = make_uint4(pk_bf16(x1[0], x1[1]), pk_bf16(x1[2], x1[3]), pk_bf16(x1[4], x1[5]), pk_bf16(x1[6], x1[7]));
-        *reinterpret_cast<uint4*>(k_hi + r0 * KS + db * 8) = h0;
-        *reinterpret_cast<uint4*>(k_hi + r1 * KS + db * 8) = h1;
-        if (PREC) {
-          const uint32_t hw0[4] = {h0.x, h0.y, h0.z, h0.w}, hw1[4] = {h1.x, h1.y, h1.z, h1.w};
-          uint32_t l0[4], l1[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            l0[i] = pk_bf16(x0[2 * i] - bf16_lo_f(hw0[i]), x0[2 * i + 1] - bf16_hi_f(hw0[i]));
-            l1[i] = pk_bf16(x1[2 * i] - bf16_lo_f(hw1[i]), x1[2 * i + 1] - bf16_hi_f(hw1[i]));
-          }
-          *reinterpret_cast<uint4*>(k_lo + r0 * KS + db * 8) = make_uint4(l0[0], l0[1], l0[2], l0[3]);
-          *reinterpret_cast<uint4*>(k_lo + r1 * KS + db * 8) = make_uint4(l1[0], l1[1], l1[2], l1[3]);
-        }
+    const bool is_v = t >= 256;
+    const int kp = is_v ? (t & 31) : ((t & 255) >> 3);
+    const int db = is_v ? ((t & 255) >> 5) : (t & 7);
+    const int r0 = 2 * kp, r1 = r0 + 1;
+    const bool ok0 = r0 < un.valid, ok1 = r1 < un.valid;
+    const uint8_t* raw = raw_buf(st, is_v ? 1 : 0);
+    if (un.bits == 16) {
+      const uint4 z = make_uint4(0, 0, 0, 0);
+      const uint4 w0 = ok0 ? bf16_row8(raw, r0, db) : z;
+      const uint4 w1 = ok1 ? bf16_row8(raw, r1, db) : z;
+      if (!is_v) {
+        uint16_t* k_hi = tile(b, 0);
+        *reinterpret_cast<uint4*>(k_hi + r0 * KS + db * 8) = w0;
+        *reinterpret_cast<uint4*>(k_hi + r1 * KS + db * 8) = w1;
       } else {
+        uint16_t* v_hi = tile(b, 1);
+        const uint32_t a0[4] = {w0.x, w0.y, w0.z, w0.w}, a1[4] = {w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const uint32_t hv = pk_bf16(x0[i], x1[i]);
-          *reinterpret_cast<uint32_t*>(v_hi + (db * 8 + i) * KS + r0) = hv;
-          if (PREC)
-            *reinterpret_cast<uint32_t*>(v_lo + (db * 8 + i) * KS + r0) =
-                pk_bf16(x0[i] - bf16_lo_f(hv), x1[i] - bf16_hi_f(hv));
+        for (int i = 0; i < 4; ++i) {
+          *reinterpret_cast<uint32_t*>(v_hi + (db * 8 + 2 * i) * KS + r0) = __builtin_amdgcn_perm(a1[i], a0[i], 0x05040100u);
+          *reinterpret_cast<uint32_t*>(v_hi + (db * 8 + 2 * i + 1) * KS + r0) = __builtin_amdgcn_perm(a1[i], a0[i], 0x07060302u);
         }
+      }
+      return;
+    }
+    float x0[8], x1[8];
+    if (ok0) dequant8(raw, un.bits, un.rows, r0, db, x0);
+    else
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x0[i] = 0.f;
+    if (ok1) dequant8(raw, un.bits, un.rows, r1, db, x1);
+    else
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x1[i] = 0.f;
+    if (!is_v) {
+      uint16_t* k_hi = tile(b, 0);
+      uint16_t* k_lo = tile(b, PREC ? 2 : 0);
+      uint4 h0, h1;
+      h0 = make_uint4(pk_bf16(x0[0], x0[1]), pk_bf16(x0[2], x0[3]), pk_bf16(x0[4], x0[5]), pk_bf16(x0[6], x0[7]));
+      h1 = make_uint4(pk_bf16(x1[0], x1[1]), pk_bf16(x1[2], x1[3]), pk_bf16(x1[4], x1[5]), pk_bf16(x1[6], x1[7]));
+      *reinterpret_cast<uint4*>(k_hi + r0 * KS + db * 8) = h0;
+      *reinterpret_cast<uint4*>(k_hi + r1 * KS + db * 8) = h1;
+      if (PREC) {
+        const uint32_t hw0[4] = {h0.x, h0.y, h0.z, h0.w}, hw1[4] = {h1.x, h1.y, h1.z, h1.w};
+        uint32_t l0[4], l1[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          l0[i] = pk_bf16(x0[2 * i] - bf16_lo_f(hw0[i]), x0[2 * i + 1] - bf16_hi_f(hw0[i]));
+          l1[i] = pk_bf16(x1[2 * i] - bf16_lo_f(hw1[i]), x1[2 * i + 1] - bf16_hi_f(hw1[i]));
+        }
+        *reinterpret_cast<uint4*>(k_lo + r0 * KS + db * 8) = make_uint4(l0[0], l0[1], l0[2], l0[3]);
+        *reinterpret_cast<uint4*>(k_lo + r1 * KS + db * 8) = make_uint4(l1[0], l1[1], l1[2], l1[3]);
+      }
+    } else {
+      uint16_t* v_hi = tile(b, 1);
+      uint16_t* v_lo = tile(b, PREC ? 3 : 1);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t hv = pk_bf16(x0[i], x1[i]);
+        *reinterpret_cast<uint32_t*>(v_hi + (db * 8 + i) * KS + r0) = hv;
+        if (PREC)
+          *reinterpret_cast<uint32_t*>(v_lo + (db * 8 + i) * KS + r0) =
+              pk_bf16(x0[i] - bf16_lo_f(hv), x1[i] - bf16_hi_f(hv));
       }
     }
   };
@@ -280,34 +355,36 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ par
 #pragma unroll
         for (int i = 0; i < 4; ++i) s[4 * j + i] = sc[nb][j][i];
       if (!full) {
+        // Visible keys of this column form one range [lo, hi) of the unit: keys
+        // below `valid`, and for a chunk piece the causal / segment window
+        // [qlo, qhi] of the query row. Lane group g holds keys base + e, e = 4 j + i.
+        const int base = 32 * kg + 8 * g;
+        const int lo = (un.chunk ? max(qlo[nb] - un.first, 0) : 0) - base;
+        const int hi = (un.chunk ? min(qhi[nb] - un.first + 1, un.valid) : un.valid) - base;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int key = 32 * kg + 8 * g + e;  // e = 4 j + i
-          bool vis = key < un.valid;
-          if (un.chunk) {
-            const int jj = un.first + key;
-            vis = vis && jj >= qlo[nb] && jj <= qhi[nb];
-          }
-          s[e] = vis ? s[e] : -INFINITY;
-        }
+        for (int e = 0; e < 8; ++e) s[e] = (e >= lo && e < hi) ? s[e] : -INFINITY;
       }
       float mt = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
-      mt = fmaxf(mt, __shfl_xor(mt, 16));
-      mt = fmaxf(mt, __shfl_xor(mt, 32));
-      const float mnew = fmaxf(m_run[nb], mt * xs);
-      const bool none = mnew == -INFINITY;
-      const float alpha = none ? 1.f : __builtin_amdgcn_exp2f(m_run[nb] - mnew);
-      const float mref = none ? 0.f : mnew;
+      const float mcand = group_max(mt) * xs;
+      // Lazy rescaling: a wave moves its running maxima (and rescales its
+      // accumulators) only when some column's max grew by more than
+      // rescale_log2; otherwise p = 2^(x - m_run) <= 2^rescale_log2.
+      if (__builtin_amdgcn_ballot_w64(mcand > m_run[nb] + rescale_log2<PREC>())) {
+        const float mnew = fmaxf(m_run[nb], mcand);
+        const float alpha = mnew == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run[nb] - mnew);
+        m_run[nb] = mnew;
+        l_part[nb] *= alpha;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) acc_o[nb][db] *= alpha;
+      }
+      const float mref = m_run[nb] == -INFINITY ? 0.f : m_run[nb];
       float p[8], psum = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         p[e] = __builtin_amdgcn_exp2f(__fmaf_rn(s[e], xs, -mref));
         psum += p[e];
       }
-      l_part[nb] = __fmaf_rn(l_part[nb], alpha, psum);
-      m_run[nb] = mnew;
-#pragma unroll
-      for (int db = 0; db < 4; ++db) acc_o[nb][db] *= alpha;
+      l_part[nb] += psum;
       const uint32_t w0 = pk_bf16(p[0], p[1]), w1 = pk_bf16(p[2], p[3]);
       const uint32_t w2 = pk_bf16(p[4], p[5]), w3 = pk_bf16(p[6], p[7]);
       p_hi[nb].u = make_uint4(w0, w1, w2, w3);
@@ -348,28 +425,29 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ par
   // So one wave's dequantization overlaps another's MFMAs, and each unit's
   // HBM latency hides behind a full iteration.
   const int n = u1 - u0;
+  uint4 win = make_uint4(0, 0, 0, 0);
+  if (u0 + lane < min(u1, a.n_tiles)) win = *reinterpret_cast<const uint4*>(a.tiles + u0 + lane);
+  auto unit = [&](int rel) { return unit_at(a, u0 + rel, rel, h, win); };
   auto stage = [&](int st, const uint4& wk, const uint4& wv) {
     *reinterpret_cast<uint4*>(raw_buf(st, 0) + padded(16 * t)) = wk;
     *reinterpret_cast<uint4*>(raw_buf(st, 1) + padded(16 * t)) = wv;
   };
-  uint4 wk, wv;
-  if (n > 0) {
-    raw_load(a, get_unit(a, u0, h), h, wk, wv);
-    stage(0, wk, wv);
-  }
-  if (n > 1) raw_load(a, get_unit(a, u0 + 1, h), h, wk, wv);
+  uint4 wk, wv, wk0, wv0;
+  if (n > 0) raw_load(a, unit(0), h, wk0, wv0);
+  if (n > 1) raw_load(a, unit(1), h, wk, wv);  // in flight while unit 0 is staged
+  if (n > 0) stage(0, wk0, wv0);
   __syncthreads();
-  if (n > 0) dequant(get_unit(a, u0, h), 0, 0);
+  if (n > 0) dequant(unit(0), 0, 0);
   if (n > 1) stage(1, wk, wv);
-  if (n > 2) raw_load(a, get_unit(a, u0 + 2, h), h, wk, wv);
+  if (n > 2) raw_load(a, unit(2), h, wk, wv);
   for (int i = 0; i < n; ++i) {
     __syncthreads();
-    if (i + 1 < n) dequant(get_unit(a, u0 + i + 1, h), (i + 1) & 1, (i + 1) & 1);
+    if (i + 1 < n) dequant(unit(i + 1), (i + 1) & 1, (i + 1) & 1);
     if (i + 2 < n) {
       stage(i & 1, wk, wv);
-      if (i + 3 < n) raw_load(a, get_unit(a, u0 + i + 3, h), h, wk, wv);
+      if (i + 3 < n) raw_load(a, unit(i + 3), h, wk, wv);
     }
-    compute(get_unit(a, u0 + i, h), i & 1);
+    compute(unit(i), i & 1);
   }
 
   // Merge the two key groups: group 1 parks (max, sum, O) in LDS (over the
@@ -379,13 +457,10 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ par
   float lsum[NBW];
 #pragma unroll
   for (int nb = 0; nb < NBW; ++nb) {
-    float l = l_part[nb];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
-    lsum[nb] = l;
+    lsum[nb] = group_sum(l_part[nb]);
   }
   float* mrg_o = reinterpret_cast<float*>(smem);
-  float2* mrg_ml = reinterpret_cast<float2*>(smem + MFMA_ROWS * D * 4);
+  float2* mrg_ml = reinterpret_cast<float2*>(smem + MFMA_ROWS * MRG_STRIDE * 4);
   __syncthreads();
   if (kg == 1 && wave_on) {
 #pragma unroll
@@ -393,7 +468,7 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ par
       const int lr = (w + 4 * nb) * 16 + col;
 #pragma unroll
       for (int db = 0; db < 4; ++db)
-        *reinterpret_cast<f32x4*>(mrg_o + lr * D + 16 * db + 4 * g) = acc_o[nb][db];
+        *reinterpret_cast<f32x4*>(mrg_o + lr * MRG_STRIDE + 16 * db + 4 * g) = acc_o[nb][db];
       if (g == 0) mrg_ml[lr] = make_float2(m_run[nb], lsum[nb]);
     }
   }
@@ -411,7 +486,7 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ par
       f32x4 o[4];
 #pragma unroll
       for (int db = 0; db < 4; ++db)
-        o[db] = acc_o[nb][db] * f0 + *reinterpret_cast<const f32x4*>(mrg_o + lr * D + 16 * db + 4 * g) * f1;
+        o[db] = acc_o[nb][db] * f0 + *reinterpret_cast<const f32x4*>(mrg_o + lr * MRG_STRIDE + 16 * db + 4 * g) * f1;
       if (r >= R) continue;
       if (splits == 1) {
         const int gq = r / a.nq, m = r - gq * a.nq;
