@@ -202,8 +202,11 @@ attn_vec_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ part
       else static_cast<uint16_t*>(a.out)[off] = (uint16_t)f32_to_bf16_rne(o);
     } else {
       const int64_t base = ((int64_t)h * splits + split) * R + r;
-      part_o[base * D + lane] = acc[i];
-      if (lane == 0) part_ml[base] = make_float2(mx[i], sm[i]);
+      __builtin_nontemporal_store(acc[i], part_o + base * D + lane);  // no dirty L2 lines at kernel end
+      if (lane == 0) {
+        __builtin_nontemporal_store(mx[i], reinterpret_cast<float*>(part_ml + base));
+        __builtin_nontemporal_store(sm[i], reinterpret_cast<float*>(part_ml + base) + 1);
+      }
     }
   }
 }
