@@ -237,7 +237,7 @@ def bench_e2e(frame_counts=(16, 64, 96), reps=2):
     from dkv.workloads import bit_schedule, candidate_lengths
     dev = torch.device('cuda:0')
     model = build_decoder(seed=0, device=dev)
-    dec = StreamingDecoder(model)
+    dec = StreamingDecoder(model, graphs=True)
     g = torch.Generator().manual_seed(0)
     vocab = model.config.vocab_size
     prefix = torch.randint(0, vocab, (1, 16), generator=g)
@@ -251,28 +251,32 @@ def bench_e2e(frame_counts=(16, 64, 96), reps=2):
         frames = [emb[i:i + 1] for i in range(nf)]
         bits = bit_schedule(nf, nf)
         best = {}
-        for proto in ('forks', 'batched'):
-            times = []
-            for _ in range(reps + 1):  # the first request warms up kernels and GEMM selection
-                torch.cuda.synchronize()
-                t0 = time.perf_counter()
-                cache = dec.ingest(prefix, frames, bits)
-                if proto == 'forks':
-                    scores = dec.answer(cache, question, cands)
-                else:
-                    scores = dec.answer_batched(cache, question, cands)
-                scores.cpu()
-                torch.cuda.synchronize()
-                times.append(time.perf_counter() - t0)
-                del cache
-            best[proto] = min(times[1:])
-        out[f'frames_{nf}'] = dict(frames_per_s_forks=round(nf / best['forks'], 2),
-                                   frames_per_s_batched=round(nf / best['batched'], 2),
-                                   request_s_forks=round(best['forks'], 4),
-                                   request_s_batched=round(best['batched'], 4),
-                                   tokens=16 + 64 * nf + 24 + sum(c.shape[1] for c in cands))
-        print(f"# e2e {nf} frames: {out[f'frames_{nf}']['frames_per_s_forks']} frames/s (forks), "
-              f"{out[f'frames_{nf}']['frames_per_s_batched']} frames/s (batched)", flush=True)
+        for graphs in (False, True):
+            dec.graphs = graphs
+            for proto in ('forks', 'batched'):
+                times = []
+                for _ in range(reps + 1):  # the first request warms up kernels, GEMM selection, the capture
+                    torch.cuda.synchronize()
+                    t0 = time.perf_counter()
+                    cache = dec.ingest(prefix, frames, bits)
+                    if proto == 'forks':
+                        scores = dec.answer(cache, question, cands)
+                    else:
+                        scores = dec.answer_batched(cache, question, cands)
+                    scores.cpu()
+                    torch.cuda.synchronize()
+                    times.append(time.perf_counter() - t0)
+                    del cache
+                best[(graphs, proto)] = min(times[1:])
+        r = out[f'frames_{nf}'] = dict(tokens=16 + 64 * nf + 24 + sum(c.shape[1] for c in cands))
+        for (graphs, proto), t in best.items():
+            tag = f"{'graph' if graphs else 'eager'}_{proto}"
+            r[f'frames_per_s_{tag}'] = round(nf / t, 2)
+            r[f'request_s_{tag}'] = round(t, 4)
+        print(f"# e2e {nf} frames: eager {r['frames_per_s_eager_forks']} / {r['frames_per_s_eager_batched']}, "
+              f"graph {r['frames_per_s_graph_forks']} / {r['frames_per_s_graph_batched']} frames/s (forks / batched)",
+              flush=True)
+    dec.graphs = False
     return out
 
 

@@ -97,12 +97,14 @@ attn_vec_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ part
   __shared__ float Vt[TILE][D];
   __shared__ float Ps[4][TILE];
 
+  const int active = runtime_plan(a, units, splits);
   const int split = blockIdx.x, h = blockIdx.y, rg = blockIdx.z;
   const int G = a.q_heads / a.heads;
   const int R = G * a.nq;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int u0 = (int)((int64_t)units * split / splits);
-  const int u1 = (int)((int64_t)units * (split + 1) / splits);
+  if (split >= active) return;  // graph replay over a shorter history than the launch bound
+  const int u0 = (int)((int64_t)units * split / active);
+  const int u1 = (int)((int64_t)units * (split + 1) / active);
   const float xs = a.scale * LOG2E;
 
   // Stage this group's query rows in LDS as fp32.
@@ -225,10 +227,12 @@ combine_kernel(dkv_attn_args a, int splits, const float* __restrict__ part_o,
   const int r = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (r >= R) return;
+  int units = 0;
+  const int active = runtime_plan(a, units, splits);  // partials written (graph replays: fewer)
   const int64_t base = (int64_t)h * splits * R + r;
   float M = -INFINITY, L = 0.f, O = 0.f;
-  for (int s0 = 0; s0 < splits; s0 += 64) {
-    const int cnt = min(64, splits - s0);
+  for (int s0 = 0; s0 < active; s0 += 64) {
+    const int cnt = min(64, active - s0);
     const float2 ml = lane < cnt ? part_ml[base + (int64_t)(s0 + lane) * R] : make_float2(-INFINITY, 0.f);
     float bm = ml.x;
 #pragma unroll

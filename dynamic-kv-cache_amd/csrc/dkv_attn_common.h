@@ -46,6 +46,20 @@ __device__ __forceinline__ Unit get_unit(const dkv_attn_args& a, int u, int h) {
   return un;
 }
 
+// Graph replays: the history bounds the kernels run with come from the device
+// step pair when one is given, and the launch-time `units` and `splits` are
+// bounds only. The splits that run are then min(splits, units), as the host
+// plan would choose for the same history, so a replay partitions the history
+// exactly like a direct call; the other workgroups exit at once and the
+// partials keep the launch's split stride. Returns the splits that run.
+__device__ __forceinline__ int runtime_plan(dkv_attn_args& a, int& units, int splits) {
+  if (!a.step) return splits;
+  a.past = a.step[0];
+  a.n_tiles = a.step[1];
+  units = a.n_tiles + (a.nq + TILE - 1) / TILE;
+  return min(splits, units);
+}
+
 // First chunk row of the segment holding chunk row j (0 when n_segs <= 1).
 __device__ __forceinline__ int chunk_seg_start(const dkv_attn_args& a, int j) {
   int start = 0;

@@ -188,6 +188,7 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ par
   auto raw_buf = [&](int st, int kv) { return smem + (st * 2 + kv) * RAWP; };
   auto tile = [&](int b, int which) { return reinterpret_cast<uint16_t*>(smem + RAW_BYTES + (b * NT + which) * TILE_BYTES); };
 
+  const int active = runtime_plan(a, units, splits);
   const int split = blockIdx.x, h = blockIdx.y, rg = blockIdx.z;
   const int G = a.q_heads / a.heads;
   const int R = G * a.nq;
@@ -195,8 +196,9 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ par
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int kg = wave >> 2, w = wave & 3;  // key group, wave within the group
   const int col = lane & 15, g = lane >> 4;
-  const int u0 = (int)((int64_t)units * split / splits);
-  const int u1 = (int)((int64_t)units * (split + 1) / splits);
+  if (split >= active) return;  // graph replay over a shorter history than the launch bound
+  const int u0 = (int)((int64_t)units * split / active);
+  const int u1 = (int)((int64_t)units * (split + 1) / active);
   const float xs = a.scale * LOG2E;
   const bool wave_on = rg * MFMA_ROWS + w * 16 < R;  // wave-uniform
 

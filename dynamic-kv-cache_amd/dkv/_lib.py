@@ -14,7 +14,7 @@ from . import _build
 
 DKV_EINVAL = -1
 DKV_MAX_CHUNK_SEGS = 16
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class Tile(ctypes.Structure):
@@ -45,7 +45,8 @@ class AttnArgs(ctypes.Structure):
                 ('out', ctypes.c_void_p), ('out_tok_stride', ctypes.c_int64), ('out_head_stride', ctypes.c_int64),
                 ('out_dtype', ctypes.c_int32), ('path', ctypes.c_int32), ('splits', ctypes.c_int32),
                 ('precision', ctypes.c_int32),
-                ('workspace', ctypes.c_void_p), ('workspace_bytes', ctypes.c_int64)]
+                ('workspace', ctypes.c_void_p), ('workspace_bytes', ctypes.c_int64),
+                ('step', ctypes.c_void_p)]
 
 
 class SegmentIO(ctypes.Structure):
@@ -87,6 +88,13 @@ SIGNATURES = [
                                          ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]),
     ('dkv_segment_validate', ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int64,
                                             ctypes.c_int32, ctypes.c_int32]),
+    ('dkv_rope_qkv', ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
+                                    ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
+                                    ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
+    ('dkv_rms_norm', ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
+                                    ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_float, ctypes.c_void_p]),
+    ('dkv_silu_mul', ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
+                                    ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]),
 ]
 
 

@@ -11,6 +11,7 @@ hand-written HIP kernels reached through libdkv's C ABI (include/dkv.h).
 """
 import bisect
 import ctypes
+import struct
 import types
 
 import torch
@@ -116,6 +117,7 @@ class GPUCache(_CacheBase):
         self.arena = torch.empty(self.arena_bytes, dtype=torch.uint8, device=self.device)
         self.tiles = torch.zeros((max(max_tiles, 1), 16), dtype=torch.uint8, device=self.device)
         self._workspace = None
+        self._graph = None  # GraphSteps while launches read their step parameters from the device
         for bits, n in planned:
             if n:
                 self._open_segment(self.segments[-1].end if self.segments else 0, n, bits)
@@ -223,6 +225,8 @@ class GPUCache(_CacheBase):
             raise ValueError('GPU cache requires CUDA, batch one and the configured head dimension')
         if k.dim() != 4 or k.shape[1] != self.heads or v.shape != k.shape or v.device != k.device:
             raise ValueError(f'append expects k and v of shape [1, {self.heads}, n, {self.dim}]')
+        if self._graph is not None:
+            return self._graph.append(k, v, layer)
         past = self.seen[layer]
         n = k.shape[-2]
         if past + n > self.capacity:
@@ -359,7 +363,10 @@ class GPUCache(_CacheBase):
             raise ValueError(f'chunk segments {segments} do not cover the {n}-token chunk')
         q, k, v = self._kv_view(q), self._kv_view(k), self._kv_view(v)
         out = torch.empty((1, n, q.shape[1], self.dim), dtype=out_dtype or q.dtype, device=q.device)
-        a = self.attend_args(q, k, v, layer, past, out, segments, path, splits, precision)
+        if self._graph is not None:
+            a = self._graph.attend_args(q, k, v, layer, out, segments, path, splits, precision)
+        else:
+            a = self.attend_args(q, k, v, layer, past, out, segments, path, splits, precision)
         lib = _lib.load()
         need = lib.dkv_attend_workspace_bytes(ctypes.byref(a))
         if need:
@@ -403,6 +410,7 @@ class GPUCache(_CacheBase):
         other.tile_starts = self.tile_starts.copy()
         other.host_counts = self.host_counts.copy()
         other._workspace = None
+        other._graph = None
         other.pending_bits = 16
         return other
 
@@ -424,6 +432,49 @@ class GPUCache(_CacheBase):
                     used_tokens=n, precision_token_counts=used,
                     arena_used_bytes=self.arena_used)
 
+
+    # -- HIP graph replays (no reference counterpart) ---------------------------
+    def begin_graph_steps(self, chunk, q_heads=None, steps=None):
+        """Switches append()/attend() to launches that read their per-step parameters from device
+        memory, so that a decoder forward over `chunk`-token chunks can be captured once in a HIP
+        graph and replayed as the history grows. Before capturing, and before every replay, call
+        graph_step(); in this mode append() and attend() only launch (no bookkeeping).
+
+        `q_heads` pre-sizes the attention workspace for the launch bounds (so nothing is allocated
+        while capturing). `steps` re-attaches the GraphSteps of an earlier capture on this cache.
+        """
+        if len(set(self.seen)) != 1:
+            raise ValueError('graph steps need every layer at the same length')
+        if steps is not None and steps.cache is not self:
+            raise ValueError('these graph steps belong to another cache')
+        self._graph = steps or GraphSteps(self, chunk)
+        if q_heads:
+            self._workspace_for(self._graph.workspace_bytes(q_heads))
+        return self._graph
+
+    def end_graph_steps(self):
+        """Back to ordinary launches; returns the GraphSteps for a later begin_graph_steps()."""
+        steps, self._graph = self._graph, None
+        return steps
+
+    def graph_step(self):
+        """Bookkeeping of one chunk for every layer (at the pending width and frame, like a layer-0
+        append) plus the upload of what the recorded launches read. Returns the history length
+        before the chunk."""
+        if self._graph is None:
+            raise ValueError('graph_step() needs begin_graph_steps()')
+        return self._graph.step()
+
+    def reset(self):
+        """Empties the cache in place, keeping its arena, tile table and device buffers (a new
+        request on a reused cache keeps every pointer a captured graph recorded)."""
+        self.seen = [0] * self.layers
+        self.cursors = [0] * self.layers
+        self.pending_bits, self.frame_id = 16, -1
+        if self.online:
+            self.segments, self.tile_starts, self.plan = [], [], []
+            self.host_counts = {4: 0, 8: 0, 16: 0}
+            self.arena_used = 0
 
     # -- the reference's serialized formats (src/kv_quantization.py:12-77, src/cache_manager.py:9-58) --
     def _layer_range(self, layers):
@@ -517,6 +568,106 @@ class GPUCache(_CacheBase):
             batch.run()
         self.seen = [end] * self.layers
         return past, batch
+
+
+class GraphSteps:
+    """Device-side step parameters of one GPUCache for HIP-graph replays.
+
+    One device buffer holds a pack job per layer (dkv_pack_batch reads layer l's job) and the
+    {past, n_tiles} pair every attention launch reads (dkv_attn_args.step). step() does the host
+    bookkeeping of one chunk and uploads the buffer through a ring of pinned host copies, so the
+    host can prepare step i+1 while the GPU still runs step i. The K/V pointers of the jobs are
+    those append() saw while the graph was captured (they are fixed for a captured graph).
+    """
+    RING = 4
+
+    def __init__(self, cache, chunk):
+        self.cache, self.chunk = cache, chunk
+        self.job_bytes = ctypes.sizeof(_lib.PackJob)
+        self.nbytes = cache.layers * self.job_bytes + 8
+        self.dev = torch.zeros(self.nbytes, dtype=torch.uint8, device=cache.device)
+        self.ring = [(torch.zeros(self.nbytes, dtype=torch.uint8, pin_memory=True), None) for _ in range(self.RING)]
+        self.slot = 0
+        self.kv = [None] * cache.layers  # (k, v) views append() recorded, kept alive with the graph
+        self.state = None  # (past, segment, write_tiles) of the current step
+        # Launch bounds: the largest history a chunk can attend to in this cache.
+        self.past_bound = cache.capacity - chunk
+        self.tiles_bound = cache.tiles.shape[0]
+
+    def step(self):
+        c, n = self.cache, self.chunk
+        past = c.seen[0]
+        if len(set(c.seen)) != 1:
+            raise ValueError('graph steps need every layer at the same length')
+        if past + n > c.capacity:
+            raise ValueError('GPU context limit exceeded')
+        if c.online:
+            seg = c._open_segment(past, n, c.pending_bits, c.frame_id)
+            write = 1
+        else:
+            seg = next((s for s in c.segments if s.start <= past < s.end), None)
+            if seg is None or past + n > seg.end or seg.bits != c.pending_bits:
+                raise ValueError(f'Cache append does not match plan at token {past}, length {n}, '
+                                 f'bits {c.pending_bits}')
+            write = int(past == seg.start)
+            if write:
+                seg.frame = c.frame_id
+        self.state = (past, seg, write)
+        c.seen = [past + n] * c.layers
+        self.upload()
+        return past
+
+    def upload(self):
+        """Writes the current step's jobs and bounds to the device buffer (async, stream-ordered)."""
+        c, n = self.cache, self.chunk
+        past, seg, write = self.state
+        jobs = (_lib.PackJob * c.layers)()
+        for l in range(c.layers):
+            kv = self.kv[l]
+            kp, vp, ks, vs = (kv[0].data_ptr(), kv[1].data_ptr(), kv[0].stride(), kv[1].stride()) if kv else \
+                (0, 0, (0, 0, 0, 0), (0, 0, 0, 0))
+            jobs[l] = _lib.PackJob(kp, vp, ks[1], ks[2], vs[1], vs[2], seg.offset, seg.rows, seg.start,
+                                   past - seg.start, n, l, seg.bits, seg.tile0, write if l == 0 else 0)
+        if all(kv is not None for kv in self.kv):
+            _lib.check(_lib.load().dkv_pack_validate(ctypes.addressof(jobs), c.layers, c.arena_bytes, c.layers,
+                                                     c.heads), 'dkv_pack_validate')
+        host, event = self.ring[self.slot]
+        if event is not None:
+            event.synchronize()  # that slot's previous copy has been consumed
+        raw = bytes(jobs) + struct.pack('<ii', past, c._tiles_before(past))
+        host.copy_(torch.frombuffer(bytearray(raw), dtype=torch.uint8))
+        self.dev.copy_(host, non_blocking=True)
+        event = torch.cuda.Event()
+        event.record()
+        self.ring[self.slot] = (host, event)
+        self.slot = (self.slot + 1) % self.RING
+
+    def append(self, k, v, layer):
+        c = self.cache
+        if self.state is None:
+            raise ValueError('graph_step() must run before the recorded append')
+        if k.shape[-2] != self.chunk:
+            raise ValueError(f'graph steps were set up for {self.chunk}-token chunks, got {k.shape[-2]}')
+        k, v = c._kv_view(k), c._kv_view(v)
+        self.kv[layer] = (k, v)
+        _lib.check(_lib.load().dkv_pack_batch(self.dev.data_ptr() + layer * self.job_bytes, 1, self.chunk,
+                                              c.arena.data_ptr(), c.arena_bytes, c.tiles.data_ptr(), c.layers,
+                                              c.heads, _lib.stream_handle(c.device)), 'dkv_pack_batch')
+        return self.state[0]
+
+    def attend_args(self, q, k, v, layer, out, segments, path, splits, precision):
+        c = self.cache
+        a = c.attend_args(q, k, v, layer, self.past_bound, out, segments, path, splits, precision)
+        a.n_tiles = self.tiles_bound
+        a.step = self.dev.data_ptr() + c.layers * self.job_bytes
+        return a
+
+    def workspace_bytes(self, q_heads):
+        a = _lib.AttnArgs()
+        a.n_tiles, a.past = self.tiles_bound, self.past_bound
+        a.layer, a.layers, a.heads, a.q_heads, a.nq = 0, self.cache.layers, self.cache.heads, q_heads, self.chunk
+        a.precision = PRECISIONS[self.cache.precision]
+        return _lib.load().dkv_attend_workspace_bytes(ctypes.byref(a))
 
 
 class SegmentExport:
@@ -629,6 +780,8 @@ def install_packed_attention(model):
     """
     from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
 
+    from .gpu_ops import rope_qkv
+
     def forward(module, hidden_states, position_embeddings=None, attention_mask=None, past_key_value=None,
                 cache_position=None, **kwargs):
         cache = past_key_value if past_key_value is not None else kwargs.get('past_key_values')
@@ -642,14 +795,23 @@ def install_packed_attention(model):
         if kwargs.get('output_attentions', False):
             raise ValueError('Fused packed attention does not expose attention matrices')
         shape = hidden_states.shape[:-1]
+        roped = None
         if fused and hasattr(module, '_qkv_weight'):
-            q, k, v = F.linear(hidden_states, module._qkv_weight).split(module._qkv_sizes, dim=-1)
+            qkv = F.linear(hidden_states, module._qkv_weight)
+            hd = module.head_dim
+            # split + RoPE in one launch (bit-equal to apply_rotary_pos_emb in bf16)
+            roped = rope_qkv(qkv, *position_embeddings, module._qkv_sizes[0] // hd, module._qkv_sizes[1] // hd, hd)
+            if roped is None:
+                q, k, v = qkv.split(module._qkv_sizes, dim=-1)
         else:
             q, k, v = module.q_proj(hidden_states), module.k_proj(hidden_states), module.v_proj(hidden_states)
-        q = q.view(*shape, -1, module.head_dim).transpose(1, 2)
-        k = k.view(*shape, -1, module.head_dim).transpose(1, 2)
-        v = v.view(*shape, -1, module.head_dim).transpose(1, 2)
-        q, k = apply_rotary_pos_emb(q, k, *position_embeddings)
+        if roped is not None:
+            q, k, v = roped
+        else:
+            q = q.view(*shape, -1, module.head_dim).transpose(1, 2)
+            k = k.view(*shape, -1, module.head_dim).transpose(1, 2)
+            v = v.view(*shape, -1, module.head_dim).transpose(1, 2)
+            q, k = apply_rotary_pos_emb(q, k, *position_embeddings)
         if fused:
             past = cache.append(k, v, module.layer_idx)
             output = cache.attend(q, k, v, module.layer_idx, past)

@@ -44,14 +44,17 @@ def build_decoder(layers=32, hidden=960, heads=15, kv_heads=5, intermediate=2560
 class StreamingDecoder:
     """Frame-by-frame ingestion into a GPUCache and candidate scoring (src/streaming.py:89-237)."""
 
-    def __init__(self, model, fused_ops=True, precision='bf16'):
+    def __init__(self, model, fused_ops=True, precision='bf16', graphs=False):
         self.model = model
         self.text = model.model
         self.config = model.config
         self.precision = precision
+        self.graphs = graphs
         self.ops_state = {'enabled': fused_ops}
         install_fused_ops(self.text, self.ops_state)
         install_packed_attention(model)
+        self._cache = None  # reused across requests when graphs=True (a captured graph records its buffers)
+        self._frame = None  # the captured frame forward
 
     @property
     def device(self):
@@ -80,21 +83,73 @@ class StreamingDecoder:
 
     @torch.inference_mode()
     def ingest(self, prefix_ids, frames, bits, cache=None, qa_reserve=256):
-        """Prefix at 16 bits, then each frame embedding [1, T, hidden] at its width (src/streaming.py:168-187)."""
+        """Prefix at 16 bits, then each frame embedding [1, T, hidden] at its width (src/streaming.py:168-187).
+
+        With graphs=True the frames after the first run as replays of one captured HIP graph of the
+        whole decoder forward (the cache's launches read their step parameters from the device), on
+        a cache the decoder keeps and resets between requests.
+        """
         if len(frames) != len(bits):
             raise ValueError('one bit width per frame')
+        total = prefix_ids.shape[1] + sum(f.shape[1] for f in frames) + qa_reserve
         if cache is None:
-            total = prefix_ids.shape[1] + sum(f.shape[1] for f in frames) + qa_reserve
-            cache = self.create_cache(total)
+            cache = self._reused_cache(total) if self.graphs else self.create_cache(total)
         cache.select(16, -1)
         self.forward(cache, ids=prefix_ids)
+        graphed = self.graphs and cache is self._cache
         for i, (emb, b) in enumerate(zip(frames, bits)):
             cache.select(b, i)
-            self.forward(cache, embeddings=emb)
+            if graphed and i > 0 and emb.shape[1] == frames[0].shape[1]:
+                self._graph_frame(cache, emb)
+            else:
+                self.forward(cache, embeddings=emb)
         cache.select(16, -1)
         if len(set(cache.seen)) != 1:
             raise RuntimeError('Decoder layers disagree about the cache length')
         return cache
+
+    def _reused_cache(self, total):
+        if self._cache is None or self._cache.capacity < total:
+            self._cache = self.create_cache(max(total, 8192))
+            self._frame = None  # a captured graph records the old cache's buffers
+        else:
+            self._cache.reset()
+        return self._cache
+
+    def _graph_frame(self, cache, emb):
+        """One frame as a replay of the captured forward (captured on first use)."""
+        fg = self._frame
+        if fg is None or fg['chunk'] != emb.shape[1]:
+            self._capture_frame(cache, emb)
+            return
+        cache.begin_graph_steps(fg['chunk'], steps=fg['steps'])
+        try:
+            past = cache.graph_step()
+            fg['emb'].copy_(emb)
+            torch.add(fg['arange'], past, out=fg['pos'][0])
+            fg['graph'].replay()
+        finally:
+            cache.end_graph_steps()
+
+    def _capture_frame(self, cache, emb):
+        chunk = emb.shape[1]
+        static_emb = emb.clone()
+        arange = torch.arange(chunk, device=self.device)
+        pos = torch.empty((1, chunk), dtype=torch.long, device=self.device)
+        steps = cache.begin_graph_steps(chunk, q_heads=self.config.num_attention_heads)
+        try:
+            past = cache.graph_step()
+            torch.add(arange, past, out=pos[0])
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                self.text(inputs_embeds=static_emb, past_key_values=cache, use_cache=True, position_ids=pos,
+                          attention_mask=None, return_dict=True)
+            steps.upload()  # the jobs now carry the K/V addresses recorded in the graph
+            graph.replay()
+        finally:
+            cache.end_graph_steps()
+        self._frame = dict(chunk=chunk, graph=graph, steps=steps, emb=static_emb, pos=pos, arange=arange)
 
     @staticmethod
     def _mean_loglik(logits, targets):

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define DKV_ABI_VERSION 1
+#define DKV_ABI_VERSION 2
 #define DKV_HEAD_DIM 64
 #define DKV_TILE_TOKENS 64
 #define DKV_MAX_CHUNK_SEGS 16
@@ -94,6 +94,10 @@ typedef struct dkv_attn_args {
                             (src/gpu_kernels.py:93-94,102); 1 = fp32-accurate */
   void* workspace;       /* device scratch of dkv_attend_workspace_bytes() */
   int64_t workspace_bytes;
+  const int32_t* step;   /* NULL, or a DEVICE pair {past, n_tiles} read when the kernels run,
+                            for launches recorded once in a HIP graph and replayed as the
+                            history grows. `past` and `n_tiles` above then bound the launch
+                            (grid, workspace) and the device pair must stay within them. */
 } dkv_attn_args;
 
 /* One segment of the arena in the reference's CPU-cache layout: what
@@ -200,6 +204,30 @@ int dkv_segment_batch(const dkv_segment_io* ios, int32_t n_ios, int32_t max_rows
  * check for one segment). No reference counterpart (see dkv_segment_batch). */
 int dkv_segment_validate(const dkv_segment_io* ios, int32_t n_ios, int32_t direction,
                          int64_t arena_bytes, int32_t layers, int32_t heads);
+
+/* Decoder pointwise ops around the path (bf16 in and out, fp32 arithmetic,
+ * 16-byte aligned buffers, row strides in elements and multiples of 8).
+ *
+ * dkv_rope_qkv: the joined Q/K/V projection [n, (q_heads + 2 kv_heads) * 64]
+ * -> q_out [q_heads, n, 64], k_out and v_out [kv_heads, n, 64], with RoPE
+ * applied to q and k exactly as transformers' apply_rotary_pos_emb computes it
+ * in bf16 (q*cos + rotate_half(q)*sin, each product and the sum rounded), from
+ * cos/sin rows [n, 64]. Replaces the split / view / apply_rotary_pos_emb steps
+ * of the reference's patched attention forward (src/gpu_cache.py:166-172). */
+int dkv_rope_qkv(const void* qkv, int64_t qkv_row_stride, const void* cos, const void* sin,
+                 int64_t cs_row_stride, int32_t n, int32_t q_heads, int32_t kv_heads,
+                 void* q_out, void* k_out, void* v_out, void* stream);
+
+/* out = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * weight) per row of `dim`
+ * elements: the reference's cuda_rms (src/gpu_ops.py:9-12) in one launch. */
+int dkv_rms_norm(const void* x, int64_t x_row_stride, const void* weight, void* out,
+                 int64_t out_row_stride, int32_t rows, int32_t dim, float eps, void* stream);
+
+/* out[:, :inter] = bf16(bf16(silu(g)) * u) for rows [g | u] of 2 * inter
+ * elements: the reference's activation_product over the joined gate/up
+ * projection (src/gpu_ops.py:14-17, 23-25) in one launch. */
+int dkv_silu_mul(const void* gate_up, int64_t row_stride, void* out, int64_t out_row_stride,
+                 int32_t rows, int32_t inter, void* stream);
 
 #ifdef __cplusplus
 }

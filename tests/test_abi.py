@@ -26,7 +26,7 @@ def test_every_declared_symbol_is_exported():
     for name in names:
         assert hasattr(lib, name), name
     assert {n for n, _, _ in _lib.SIGNATURES} == set(names)
-    assert lib.dkv_version() == 1
+    assert lib.dkv_version() == 2
 
 
 STRUCT_PROBE = r'''
@@ -218,3 +218,17 @@ def test_segment_io_payload_alignment_and_tile_table():
     assert lib.dkv_segment_validate(ctypes.addressof(neg), 1, 1, 1 << 20, 2, 5) == _lib.DKV_EINVAL
     assert lib.dkv_segment_batch(ctypes.addressof(table), 2, 64, 2, 2, ctypes.c_void_p(4096), 1 << 20, None, 2, 5,
                                  None) == _lib.DKV_EINVAL
+
+
+def test_pointwise_ops_reject_misaligned_buffers():
+    lib = _lib.load()
+    ok = ctypes.c_void_p(4096)
+    bad = ctypes.c_void_p(4098)
+    assert lib.dkv_rope_qkv(bad, 1600, ok, ok, 64, 4, 15, 5, ok, ok, ok, None) == _lib.DKV_EINVAL
+    assert lib.dkv_rope_qkv(ok, 1000, ok, ok, 64, 4, 15, 5, ok, ok, ok, None) == _lib.DKV_EINVAL  # row too short
+    assert lib.dkv_rms_norm(ok, 960, ok, ok, 960, 4, 12, 1e-5, None) == _lib.DKV_EINVAL  # dim % 8
+    assert lib.dkv_rms_norm(ok, 964, ok, ok, 960, 4, 960, 1e-5, None) == _lib.DKV_EINVAL  # stride % 8
+    assert lib.dkv_silu_mul(ok, 5120, bad, 2560, 4, 2560, None) == _lib.DKV_EINVAL
+    assert lib.dkv_silu_mul(ok, 4000, ok, 2560, 4, 2560, None) == _lib.DKV_EINVAL  # row holds < 2 * inter
+    assert 'dkv_silu_mul' in lib.dkv_last_error().decode()
+    assert lib.dkv_rms_norm(ok, 960, ok, ok, 960, 0, 960, 1e-5, None) == 0  # no rows: nothing to launch

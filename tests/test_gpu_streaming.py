@@ -91,3 +91,40 @@ def test_mixed_width_ingest_tracks_the_schedule(cuda):
     assert [s.bits for s in cache.segments] == [16] + bits
     logits = dec.forward(cache, ids=torch.randint(0, 512, (1, 8)), logits=8)
     assert torch.isfinite(logits).all()
+
+
+def test_graph_replayed_ingest_matches_eager(cuda):
+    """Frames 2..n replay one captured HIP graph of the decoder forward (launches read their step
+    parameters from the device, and the attention runs the splits the host plan would choose for
+    the current history). The cache bookkeeping, the packed bytes and the logits must equal the
+    eager ingest's exactly, and a second request that reuses the captured graph on the reset
+    cache must reproduce the first bit for bit."""
+    announce('streaming: graph-replayed ingest vs eager, two requests')
+    model = build_decoder(**SMALL, seed=12)
+    dec = StreamingDecoder(model, precision='fp32')
+    g = torch.Generator().manual_seed(13)
+    prefix = torch.randint(0, 512, (1, 16), generator=g)
+    question = torch.randint(0, 512, (1, 24), generator=g)
+    bits = [4, 8, 16, 4, 8, 4]
+    frames = frames_for(model, len(bits), seed=14)
+
+    def run():
+        cache = dec.ingest(prefix, frames, bits)
+        logits = dec.forward(cache.fork(), ids=question, logits=question.shape[1])
+        torch.cuda.synchronize()
+        return cache, logits
+
+    eager_cache, eager = run()
+    dec.graphs = True
+    graph_cache, first = run()
+    assert dec._frame is not None and graph_cache is dec._cache
+    assert graph_cache.plan == eager_cache.plan and graph_cache.seen == eager_cache.seen
+    assert [s.frame for s in graph_cache.segments] == [s.frame for s in eager_cache.segments]
+    assert graph_cache.accounting()['precision_token_counts'] == eager_cache.accounting()['precision_token_counts']
+    for layer in (0, SMALL['layers'] - 1):
+        for a, b in zip(graph_cache.materialize(layer), eager_cache.materialize(layer)):
+            assert torch.equal(a, b)
+    assert torch.equal(first, eager), (first - eager).abs().max().item()
+    _, second = run()
+    assert torch.equal(first, second)
+    dec.graphs = False
