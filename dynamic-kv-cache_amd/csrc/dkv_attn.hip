@@ -97,7 +97,8 @@ attn_vec_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ part
   __shared__ float Vt[TILE][D];
   __shared__ float Ps[4][TILE];
 
-  const int active = runtime_plan(a, units, splits);
+  Hist hs;
+  const int active = runtime_plan(a, hs, units, splits);
   const int split = blockIdx.x, h = blockIdx.y, rg = blockIdx.z;
   const int G = a.q_heads / a.heads;
   const int R = G * a.nq;
@@ -137,7 +138,7 @@ attn_vec_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ part
   }
 
   for (int u = u0; u < u1; ++u) {
-    const Unit un = get_unit(a, u, h);
+    const Unit un = get_unit(a, hs, u, h);
     __syncthreads();  // previous unit's readers are done; Qs is staged
     {
       const int r = tid >> 2, c = tid & 3;
@@ -228,7 +229,8 @@ combine_kernel(dkv_attn_args a, int splits, const float* __restrict__ part_o,
   const int lane = threadIdx.x & 63;
   if (r >= R) return;
   int units = 0;
-  const int active = runtime_plan(a, units, splits);  // partials written (graph replays: fewer)
+  Hist hs;
+  const int active = runtime_plan(a, hs, units, splits);  // partials written (graph replays: fewer)
   const int64_t base = (int64_t)h * splits * R + r;
   float M = -INFINITY, L = 0.f, O = 0.f;
   for (int s0 = 0; s0 < active; s0 += 64) {

@@ -21,13 +21,20 @@ struct Unit {
   const uint8_t* vsub;
 };
 
-__device__ __forceinline__ Unit get_unit(const dkv_attn_args& a, int u, int h) {
+// The history a launch attends to: the args' own bounds, or (graph replays)
+// the device step pair. Kept apart from the by-value kernel args, which the
+// kernels never write (a written copy would be spilled to scratch).
+struct Hist {
+  int past, n_tiles;
+};
+
+__device__ __forceinline__ Unit get_unit(const dkv_attn_args& a, const Hist& hs, int u, int h) {
   Unit un;
-  if (u < a.n_tiles) {
+  if (u < hs.n_tiles) {
     const dkv_tile t = a.tiles[u];
     un.chunk = false;
     un.first = t.token_start;
-    un.valid = min((int)t.rows, a.past - t.token_start);
+    un.valid = min((int)t.rows, hs.past - t.token_start);
     un.bits = t.bits;
     un.rows = t.rows;
     const int64_t sb = subblock_bytes(t.rows, t.bits);
@@ -35,7 +42,7 @@ __device__ __forceinline__ Unit get_unit(const dkv_attn_args& a, int u, int h) {
     un.ksub = base + ((int64_t)(a.layer * 2 + 0) * a.heads + h) * sb;
     un.vsub = base + ((int64_t)(a.layer * 2 + 1) * a.heads + h) * sb;
   } else {
-    const int c = u - a.n_tiles;
+    const int c = u - hs.n_tiles;
     un.chunk = true;
     un.first = c * TILE;
     un.valid = min(TILE, a.nq - c * TILE);
@@ -52,11 +59,13 @@ __device__ __forceinline__ Unit get_unit(const dkv_attn_args& a, int u, int h) {
 // plan would choose for the same history, so a replay partitions the history
 // exactly like a direct call; the other workgroups exit at once and the
 // partials keep the launch's split stride. Returns the splits that run.
-__device__ __forceinline__ int runtime_plan(dkv_attn_args& a, int& units, int splits) {
+__device__ __forceinline__ int runtime_plan(const dkv_attn_args& a, Hist& hs, int& units, int splits) {
+  hs.past = a.past;
+  hs.n_tiles = a.n_tiles;
   if (!a.step) return splits;
-  a.past = a.step[0];
-  a.n_tiles = a.step[1];
-  units = a.n_tiles + (a.nq + TILE - 1) / TILE;
+  hs.past = a.step[0];
+  hs.n_tiles = a.step[1];
+  units = hs.n_tiles + (a.nq + TILE - 1) / TILE;
   return min(splits, units);
 }
 

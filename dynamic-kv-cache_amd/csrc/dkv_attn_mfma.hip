@@ -148,8 +148,9 @@ __device__ __forceinline__ void raw_load(const dkv_attn_args& a, const Unit& un,
 // range come from `win`, the descriptors every wave loaded with one vector load
 // at kernel start (lane i holds unit u0 + i), so the unit walk never waits on a
 // scalar load; later tiles fall back to reading the table.
-__device__ __forceinline__ Unit unit_at(const dkv_attn_args& a, int u, int rel, int h, const uint4& win) {
-  if (u >= a.n_tiles || rel >= 64) return get_unit(a, u, h);
+__device__ __forceinline__ Unit unit_at(const dkv_attn_args& a, const Hist& hs, int u, int rel, int h,
+                                        const uint4& win) {
+  if (u >= hs.n_tiles || rel >= 64) return get_unit(a, hs, u, h);
   Unit un;
   const int64_t off = (int64_t)((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)win.y, rel) << 32 |
                                 (uint32_t)__builtin_amdgcn_readlane((int)win.x, rel));
@@ -158,7 +159,7 @@ __device__ __forceinline__ Unit unit_at(const dkv_attn_args& a, int u, int rel, 
   const int rows = (int)(w3 & 0xffffu), bits = (int)((w3 >> 16) & 0xffu);
   un.chunk = false;
   un.first = tok;
-  un.valid = min(rows, a.past - tok);
+  un.valid = min(rows, hs.past - tok);
   un.bits = bits;
   un.rows = rows;
   const int64_t sb = subblock_bytes(rows, bits);
@@ -188,7 +189,8 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ par
   auto raw_buf = [&](int st, int kv) { return smem + (st * 2 + kv) * RAWP; };
   auto tile = [&](int b, int which) { return reinterpret_cast<uint16_t*>(smem + RAW_BYTES + (b * NT + which) * TILE_BYTES); };
 
-  const int active = runtime_plan(a, units, splits);
+  Hist hs;
+  const int active = runtime_plan(a, hs, units, splits);
   const int split = blockIdx.x, h = blockIdx.y, rg = blockIdx.z;
   const int G = a.q_heads / a.heads;
   const int R = G * a.nq;
@@ -430,8 +432,8 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ par
   // HBM latency hides behind a full iteration.
   const int n = u1 - u0;
   uint4 win = make_uint4(0, 0, 0, 0);
-  if (u0 + lane < min(u1, a.n_tiles)) win = *reinterpret_cast<const uint4*>(a.tiles + u0 + lane);
-  auto unit = [&](int rel) { return unit_at(a, u0 + rel, rel, h, win); };
+  if (u0 + lane < min(u1, hs.n_tiles)) win = *reinterpret_cast<const uint4*>(a.tiles + u0 + lane);
+  auto unit = [&](int rel) { return unit_at(a, hs, u0 + rel, rel, h, win); };
   auto stage = [&](int st, const uint4& wk, const uint4& wv) {
     *reinterpret_cast<uint4*>(raw_buf(st, 0) + padded(16 * t)) = wk;
     *reinterpret_cast<uint4*>(raw_buf(st, 1) + padded(16 * t)) = wv;

@@ -51,8 +51,10 @@ __device__ __forceinline__ void io_wave(const dkv_segment_io& s, int w, uint8_t*
   uint8_t* arow[IO_UNITS];
   uint8_t* pay[IO_UNITS];
   float2* meta[IO_UNITS];
+  float* offp[IO_UNITS];
+  float* sclp[IO_UNITS];
   int64_t buf_row[IO_UNITS];
-  int nrows[IO_UNITS], kvs[IO_UNITS];
+  int nrows[IO_UNITS];
 #pragma unroll
   for (int q = 0; q < IO_UNITS; ++q) {
     const int u = u0 + q;
@@ -65,13 +67,16 @@ __device__ __forceinline__ void io_wave(const dkv_segment_io& s, int w, uint8_t*
     const int lo = max(t * TILE, s.row0);  // segment rows this sub-block moves: [lo, hi)
     const int hi = min(t * TILE + tile_rows, s.row0 + s.rows);
     nrows[q] = u < units ? max(hi - lo, 0) : 0;
-    kvs[q] = kv;
     uint8_t* sub = arena + s.seg_offset + (int64_t)t * slab +
                    ((int64_t)((s.layer0 + li) * 2 + kv) * heads + h) * subblock_bytes(tile_rows, bits);
     buf_row[q] = ((int64_t)li * heads + h) * s.rows + (lo - s.row0);
-    pay[q] = static_cast<uint8_t*>(s.payload[kv]) + buf_row[q] * rb;
+    // (fields picked with selects, not a runtime index: an indexed copy of the
+    // table entry would live in scratch memory)
+    pay[q] = static_cast<uint8_t*>(kv ? s.payload[1] : s.payload[0]) + buf_row[q] * rb;
     arow[q] = sub + (int64_t)(lo - t * TILE) * rb;
     meta[q] = reinterpret_cast<float2*>(sub + (int64_t)tile_rows * rb) + (lo - t * TILE);
+    offp[q] = (kv ? s.offsets[1] : s.offsets[0]) + buf_row[q];
+    sclp[q] = (kv ? s.scales[1] : s.scales[0]) + buf_row[q];
     const int nvec = nrows[q] * rb / 16;
     const u32x4* src = reinterpret_cast<const u32x4*>(IMPORT ? pay[q] : arow[q]);
 #pragma unroll
@@ -81,7 +86,7 @@ __device__ __forceinline__ void io_wave(const dkv_segment_io& s, int w, uint8_t*
     }
     if (bits < 16 && lane < nrows[q]) {
       if (IMPORT)
-        m[q] = make_float2(s.offsets[kv][buf_row[q] + lane], s.scales[kv][buf_row[q] + lane]);
+        m[q] = make_float2(offp[q][lane], sclp[q][lane]);
       else
         m[q] = meta[q][lane];
     }
@@ -99,8 +104,8 @@ __device__ __forceinline__ void io_wave(const dkv_segment_io& s, int w, uint8_t*
       if (IMPORT) {
         meta[q][lane] = m[q];
       } else {
-        s.offsets[kvs[q]][buf_row[q] + lane] = m[q].x;
-        s.scales[kvs[q]][buf_row[q] + lane] = m[q].y;
+        offp[q][lane] = m[q].x;
+        sclp[q][lane] = m[q].y;
       }
     }
   }
