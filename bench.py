@@ -207,7 +207,15 @@ def bench_attention(past, steps, warmup, rotate, precision='bf16'):
     flops = attention_flops(past, [64])
     del keep
     return dict(us_per_layer=ms * 1e3, gbs=nbytes / (ms * 1e-3) / 1e9, tflops=flops / (ms * 1e-3) / 1e12,
-                bytes=nbytes, flops=flops, mfma_frac=flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS)
+                bytes=nbytes, flops=flops, mfma_frac=flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+                hbm_frac=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, **attainable(nbytes, flops, ms))
+
+
+def attainable(nbytes, flops, ms):
+    """The roofline time min over (HBM, bf16 MFMA) bounds, max(bytes/8 TB/s, flops/2.5 PFLOP/s), and the
+    measured time's fraction of it (the attainable roofline of a mixed-intensity workload)."""
+    t = max(nbytes / (HBM_PEAK_GBS * 1e9), flops / (BF16_PEAK_TFLOPS * 1e12))
+    return dict(roofline_us=t * 1e6, attainable_frac=t / (ms * 1e-3))
 
 
 def bench_candidates(bits, steps, warmup, rotate, precision='bf16'):
@@ -223,7 +231,8 @@ def bench_candidates(bits, steps, warmup, rotate, precision='bf16'):
     flops = attention_flops(past, lengths)
     del keep
     return dict(us_per_batch=ms * 1e3, gbs=nbytes / (ms * 1e-3) / 1e9, tflops=flops / (ms * 1e-3) / 1e12,
-                bytes=nbytes, flops=flops, lengths=lengths, hbm_frac=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS)
+                bytes=nbytes, flops=flops, lengths=lengths, hbm_frac=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                mfma_frac=flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, **attainable(nbytes, flops, ms))
 
 
 def bench_e2e(frame_counts=(16, 64, 96), reps=2):
