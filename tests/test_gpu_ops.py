@@ -84,3 +84,31 @@ def test_uncovered_inputs_take_the_reference_composition(cuda):
     w = torch.rand((40,), device=cuda)
     assert torch.equal(gpu_ops.cuda_rms(x, w, 1e-6), torch.nn.functional.rms_norm(x, (40,), None, 1e-6) * w)
     assert gpu_ops.rope_qkv(x[None], x[None, :, :64 - 24], x[None, :, :40], 1, 1) is None
+
+
+@pytest.mark.parametrize('dim', [576, 960])
+def test_cuda_rms_matches_upstream_reference_bounds(cuda, dim):
+    """Port of tests/test_gpu_backend.py:103-109 with its own bounds (max .063, mean .001)."""
+    announce(f'ops: reference rms bounds dim={dim}')
+    torch.manual_seed(dim)
+    x = torch.randn(1, 19, dim, device=cuda, dtype=torch.bfloat16)
+    weight = torch.randn(dim, device=cuda, dtype=torch.bfloat16)
+    reference = weight * (x.float() * torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + 1e-5)).bfloat16()
+    actual = gpu_ops.cuda_rms(x, weight, 1e-5)
+    diff = (reference.float() - actual.float()).abs()
+    assert diff.max() < .063 and diff.mean() < .001
+
+
+def test_fused_activation_matches_upstream_reference_bounds(cuda):
+    """Port of tests/test_gpu_backend.py:111-122 with its own bounds."""
+    announce('ops: reference activation bounds')
+    torch.manual_seed(23)
+    gate = torch.randn(1, 23, 2560, device=cuda, dtype=torch.bfloat16)
+    up = torch.randn_like(gate)
+    expected = torch.nn.functional.silu(gate) * up
+    diff = (expected.float() - gpu_ops.activation_product(gate, up).float()).abs()
+    assert diff.max() < .063 and diff.mean() < .001
+    joined = torch.randn(1, 23, 5120, device=cuda, dtype=torch.bfloat16)
+    gate, up = joined.chunk(2, -1)
+    expected = torch.nn.functional.silu(gate) * up
+    assert torch.allclose(gpu_ops.activation_product(gate, up), expected, atol=.063, rtol=.01)
