@@ -10,7 +10,8 @@ place of the vision encoder:
   over the packed history (install_packed_attention).
 - answer(): the reference's 'candidate' protocol (src/streaming.py:209-225).
   For each candidate, a fork of the cache runs question + candidate tokens, and
-  the score is the mean log-likelihood of the candidate tokens.
+  the score is the mean log-likelihood of the candidate tokens. answer_labels()
+  is the 'label' protocol and prior_scores() the prior of 'candidate_calibrated'.
 - answer_batched(): the same scores from one forward of the question on a fork,
   then one forward of all candidates together. The candidates sit back to back
   in one chunk with per-candidate positions and a block-diagonal chunk mask
@@ -165,6 +166,25 @@ class StreamingDecoder:
             lg = self.forward(branch, ids=ids, logits=cand.shape[1] + 1)
             scores.append(self._mean_loglik(lg[0, :-1], cand[0].to(self.device)))
         return torch.stack(scores)
+
+    @torch.inference_mode()
+    def answer_labels(self, cache, question_ids, label_ids):
+        """The reference's 'label' protocol (src/streaming.py:202-208): one forward of the question
+        on a fork; the scores are the last position's logits at the option-label token ids."""
+        branch = cache.fork()
+        logits = self.forward(branch, ids=question_ids, logits=1)[0, -1]
+        return logits[torch.as_tensor(label_ids, device=self.device)]
+
+    @torch.inference_mode()
+    def prior_scores(self, prefix_ids, question_ids, candidates):
+        """Candidate scores without the video, for the 'candidate_calibrated' protocol
+        (src/streaming.py:124-127, 226-233): the same scoring on a cache holding only the prefix.
+        Calibrated scores are answer(...) - prior_scores(...)."""
+        total = prefix_ids.shape[1] + question_ids.shape[1] + max(c.shape[1] for c in candidates) + 64
+        cache = self.create_cache(total)
+        cache.select(16, -1)
+        self.forward(cache, ids=prefix_ids)
+        return self.answer(cache, question_ids, candidates)
 
     @torch.inference_mode()
     def answer_batched(self, cache, question_ids, candidates):

@@ -128,3 +128,30 @@ def test_graph_replayed_ingest_matches_eager(cuda):
     _, second = run()
     assert torch.equal(first, second)
     dec.graphs = False
+
+
+def test_label_protocol_and_calibration_prior(cuda):
+    """The 'label' protocol reads the last position's logits at the label ids on a fork (the base
+    cache keeps its length), and the calibration prior is the candidate scoring on a prefix-only
+    cache: it must equal answer() on such a cache built by hand."""
+    announce('streaming: label protocol and calibration prior')
+    model = build_decoder(**SMALL, seed=15)
+    dec = StreamingDecoder(model, precision='fp32')
+    g = torch.Generator().manual_seed(16)
+    prefix = torch.randint(0, 512, (1, 16), generator=g)
+    question = torch.randint(0, 512, (1, 20), generator=g)
+    labels = [3, 77, 101, 250]
+    cache = dec.ingest(prefix, frames_for(model, 3, seed=17), [4, 8, 16])
+    seen = cache.get_seq_length()
+    got = dec.answer_labels(cache, question, labels)
+    full = dec.forward(cache.fork(), ids=question, logits=1)[0, -1]
+    torch.cuda.synchronize()
+    assert cache.get_seq_length() == seen
+    assert torch.equal(got, full[torch.tensor(labels, device=full.device)])
+    cands = [torch.randint(0, 512, (1, n), generator=g) for n in (9, 13)]
+    prior = dec.prior_scores(prefix, question, cands)
+    bare = dec.create_cache(128)
+    bare.select(16, -1)
+    dec.forward(bare, ids=prefix)
+    torch.cuda.synchronize()
+    assert torch.equal(prior, dec.answer(bare, question, cands))
