@@ -76,8 +76,11 @@ def reference_semantics(q, k, v, past, scale=0.125, block=64, segments=None, out
         s = (qf @ kb[:, b0:b1].transpose(1, 2)) * scale
         s = s.masked_fill(~mask[None, :, b0:b1], float('-inf'))
         new = torch.maximum(mx, s.amax(-1))
-        alpha = torch.exp(mx - new)
-        p = torch.exp(s - new[..., None])
+        # A row with no visible key yet (only possible with chunk segments, which the reference
+        # does not have) keeps its empty state instead of exp(-inf - -inf) = nan.
+        ref = torch.where(new == float('-inf'), torch.zeros_like(new), new)
+        alpha = torch.exp(mx - ref)
+        p = torch.exp(s - ref[..., None])
         den = den * alpha + p.sum(-1)
         acc = acc * alpha[..., None] + p.to(torch.bfloat16).float() @ vb[:, b0:b1]
         mx = new

@@ -7,7 +7,9 @@ Tolerances:
   precision='bf16' (the reference kernel's rounding of K, V and p to bf16) vs the emulated
     reference kernel (oracle.attention.reference_semantics):
     - one split (the reference's own key order, so p is rounded against the same running max):
-      fp32 output max-abs <= 2e-2;
+      fp32 output max-abs <= 2e-2 on the metric's frame-chunk and candidate workloads. The MFMA
+      kernel's two key groups keep running maxima over 32 keys of each unit, so the seeded
+      random-shape sweep bounds one split like the default split below;
     - the default split history: each split rounds p against its own running max, so the result
       also carries the reference's own dependence on where its 64-key blocks fall. The bound is
       2e-2 plus that dependence measured on the same input (reference at 32-key blocks vs 64-key
@@ -46,6 +48,8 @@ def build(case, cuda, layers=1, plan_mode=False):
         for src, dst in ((k, dk), (v, dv)):
             dst.append(dequant_rows(*pack_rows(src, b), b))
         t0 += n
+    if not dk:  # no history
+        return c, case['k_hist'].float(), case['v_hist'].float()
     return c, torch.cat(dk, 1), torch.cat(dv, 1)
 
 
@@ -264,3 +268,46 @@ def test_sequential_mixed_appends_script_scenario(cuda):
             full_k, full_v = cache.materialize(0)
             if bits == 16:
                 assert torch.equal(full_k[:, :, -n:], k)
+
+
+def random_configs(count=24, seed=2024):
+    """Seeded shapes beyond the metric's: KV heads 1-8, GQA groups 1-4, chunks 1-130, histories that
+    end inside a tile, random chunk segmentations, both precisions and paths."""
+    import random
+    rng = random.Random(seed)
+    out = []
+    for i in range(count):
+        heads = rng.choice([1, 2, 3, 5, 8])
+        group = rng.choice([1, 2, 3, 4])
+        nq = rng.choice([1, 2, 7, 16, 33, 64, 65, 130])
+        past = rng.choice([0, 1, 63, 64, 65, 200, 700, 1500])
+        cuts = sorted(rng.sample(range(1, nq), min(nq - 1, rng.randint(0, 3)))) if nq > 1 else []
+        segments = [0] + cuts + [nq] if cuts else None
+        out.append((i, heads, group, nq, past, segments, rng.choice(['fp32', 'bf16']), rng.choice(PATHS + ['auto'])))
+    return out
+
+
+@pytest.mark.parametrize('i,heads,group,nq,past,segments,precision,path', random_configs())
+def test_random_shapes_against_the_oracles(cuda, i, heads, group, nq, past, segments, precision, path):
+    """fp32 precision within 1e-3 of the fp64 oracle; bf16 at one split within 2e-2 of the emulated
+    reference plus the reference's own 32-vs-64-key block sensitivity on the same input (the MFMA
+    kernel's two key groups each keep a running max over 32 keys of every unit, which rounds p like
+    the reference would at 32-key blocks), on unit-normal data with outlier channels."""
+    announce(f'attention random config {i}: heads={heads} group={group} nq={nq} past={past} '
+             f'segments={segments} precision={precision} path={path}')
+    case = frame_chunk_case(past, seed=100 + i, heads=heads, q_heads=heads * group, nq=nq)
+    c, dk, dv = build(case, cuda)
+    if precision == 'fp32':
+        got = run(c, case, cuda, torch.float32, segments=segments, path=path)
+        ref = oracle_out(case, dk, dv, segments)
+        err = (got - ref).abs().max().item()
+        assert err <= 1e-3, err
+    else:
+        q, kn, vn = (case[x][None].to(cuda) for x in ('q', 'k_new', 'v_new'))
+        c.select(16)
+        p0 = c.append(kn, vn, 0)
+        got = c.attend(q, kn, vn, 0, p0, out_dtype=torch.float32, segments=segments, path=path, splits=1,
+                       precision='bf16')[0].cpu().double()
+        ref = semantics_out(case, dk, dv, segments, torch.float32)
+        err = (got - ref).abs().max().item()
+        assert err <= 2e-2 + block_sensitivity(case, dk, dv, segments), err

@@ -158,3 +158,18 @@ def test_reference_semantics_segments_equal_separate_calls():
         vc = torch.cat((v[:, :past], v[:, past + lo:past + hi]), 1)
         alone = reference_semantics(q[:, lo:hi], kc, vc, past, out_dtype=torch.float32)
         assert torch.allclose(got[lo:hi], alone, atol=1e-6)
+
+
+def test_reference_semantics_skips_blocks_a_segment_cannot_see():
+    """With chunk segments a row's first key blocks can be fully masked (never so in the reference,
+    whose chunk is one causal segment): the emulation must keep the empty state there (no nan) and
+    stay within bf16 rounding of the exact oracle."""
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn((2, 65, 64), generator=g).to(torch.bfloat16)
+    k = torch.randn((1, 65, 64), generator=g)
+    v = torch.randn((1, 65, 64), generator=g)
+    exact = attention(q, k, v, 0, segments=[0, 60, 65])
+    for block in (16, 32, 64):
+        got = reference_semantics(q, k, v, 0, block=block, segments=[0, 60, 65], out_dtype=torch.float32)
+        assert not torch.isnan(got).any()
+        assert (got.double() - exact).abs().max().item() <= 2e-2
