@@ -218,6 +218,18 @@ def attainable(nbytes, flops, ms):
     return dict(roofline_us=t * 1e6, attainable_frac=t / (ms * 1e-3))
 
 
+def bench_decode(past, nq, steps, warmup, rotate, precision='bf16'):
+    """A short chunk (nq = 1: one decode token) over a mixed history; us per layer."""
+    from dkv.workloads import bit_schedule
+    bits = bit_schedule(past, (past + TILE - 1) // TILE)
+    replay, nbytes, keep = attention_setup(past, rotate, bits, nq=nq, seed=past + nq, precision=precision)
+    ms = time_launches(replay, max(1, steps // 10), max(1, warmup // 10)) / rotate
+    flops = attention_flops(past, [nq])
+    del keep
+    return dict(us_per_layer=ms * 1e3, gbs=nbytes / (ms * 1e-3) / 1e9, bytes=nbytes,
+                hbm_frac=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, **attainable(nbytes, flops, ms))
+
+
 def bench_candidates(bits, steps, warmup, rotate, precision='bf16'):
     from dkv.workloads import candidate_lengths
     lengths = candidate_lengths(0, 4)
@@ -363,6 +375,14 @@ def main():
                 res['attention'][f'{prec}_past_{past}'] = r
                 print(f"# attn {prec} past={past}: {r['us_per_layer']:.2f} us/layer, {r['gbs']:.0f} GB/s, "
                       f"{r['tflops']:.1f} TFLOP/s", flush=True)
+    if args.only in ('attn', 'all'):
+        res['decode'] = {}
+        for prec in ('bf16', 'fp32'):
+            for nq in (1, 4):
+                r = bench_decode(8128, nq, args.steps, args.warmup, args.rotate, prec)
+                res['decode'][f'{prec}_past_8128_nq_{nq}'] = r
+                print(f"# decode {prec} past=8128 nq={nq}: {r['us_per_layer']:.2f} us/layer, {r['gbs']:.0f} GB/s",
+                      flush=True)
     if args.only in ('cand', 'all'):
         res['candidates'] = {}
         for prec in ('bf16', 'fp32'):
@@ -392,6 +412,9 @@ def main():
     if 'attention' in res:
         line['attention'] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in r.items()}
                              for k, r in res['attention'].items()}
+    if 'decode' in res:
+        line['decode'] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in r.items()}
+                          for k, r in res['decode'].items()}
     if 'candidates' in res:
         line['candidates'] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in r.items()}
                               for k, r in res['candidates'].items()}

@@ -81,8 +81,8 @@ __device__ __forceinline__ float wave_sum(float v) {
 __device__ __forceinline__ float round_bf16(float x) { return __uint_as_float(f32_to_bf16_rne(x) << 16); }
 
 // ---------------------------------------------------------------------------
-// Vector path, for query chunks too short for MFMA tiles (fewer than 16 rows
-// per KV head, e.g. one decode token). A wave owns VEC_RPW query rows; lane n
+// Vector path (path 1, on request): fp32 FMA instead of MFMA tiles, kept as a
+// second implementation the MFMA kernel is checked against. A wave owns VEC_RPW query rows; lane n
 // scores key n of the unit, lane d accumulates output column d. PREC 0 rounds
 // the dequantized K/V and p to bf16 where the reference kernel does
 // (src/gpu_kernels.py:93-94,102); PREC 1 stays in fp32 throughout.
@@ -326,7 +326,10 @@ static Plan make_plan(const dkv_attn_args& a) {
   const int G = a.q_heads / a.heads;
   const int R = G * a.nq;
   p.path = a.path;
-  if (p.path == 0) p.path = R >= 16 ? 2 : 1;
+  // Auto takes the MFMA kernel for every chunk length: even a one-token decode step (3 rows per
+  // KV head, 13 of every 16 MFMA rows idle) runs in half the vector kernel's time at long
+  // histories, because the MFMA kernel's unit pipeline is what bounds both.
+  if (p.path == 0) p.path = 2;
   p.precision = a.precision;
   p.rows_per_group = p.path == 2 ? MFMA_ROWS : VEC_ROWS;
   p.row_groups = (R + p.rows_per_group - 1) / p.rows_per_group;

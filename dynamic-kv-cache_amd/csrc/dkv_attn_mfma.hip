@@ -1,6 +1,7 @@
 // MFMA path of the fused packed-history attention (gfx950,
-// v_mfma_f32_16x16x32_bf16), used when a KV head has at least 16 query rows
-// (a 64-token frame chunk times 3 GQA heads gives 192).
+// v_mfma_f32_16x16x32_bf16), used for every chunk length: a 64-token frame
+// chunk times 3 GQA heads gives 192 query rows per KV head; a one-token decode
+// step fills 3 of the 16 rows of one block.
 //
 // Workgroup = 8 waves = one KV head, up to 192 query rows (every GQA head of
 // that KV head), one contiguous range of units (64-key history tiles, then

@@ -341,7 +341,7 @@ class GPUCache(_CacheBase):
 
         `segments` (optional) lists chunk boundaries [0, b1, ..., nq] for a block-diagonal batch of
         independent continuations that share the history, e.g. QA candidates. `path` is 'auto'
-        (MFMA once a KV head has 16 query rows), 'vector' or 'mfma'; `precision` overrides the
+        (the MFMA kernel for every chunk length), 'vector' or 'mfma'; `precision` overrides the
         cache's 'bf16' / 'fp32' setting for this call.
         """
         if precision is not None and precision not in PRECISIONS:

@@ -88,7 +88,7 @@ typedef struct dkv_attn_args {
   void* out;             /* [nq, q_heads, 64] with the strides below */
   int64_t out_tok_stride, out_head_stride;
   int32_t out_dtype;     /* 0 = bf16, 1 = fp32 */
-  int32_t path;          /* 0 = auto (MFMA when q_heads/heads * nq >= 16), 1 = vector, 2 = MFMA */
+  int32_t path;          /* 0 = auto (the MFMA kernel), 1 = vector, 2 = MFMA */
   int32_t splits;        /* 0 = auto; history split count per KV head */
   int32_t precision;     /* 0 = the reference kernel's bf16 rounding of K, V and p
                             (src/gpu_kernels.py:93-94,102); 1 = fp32-accurate */
