@@ -78,8 +78,6 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-__device__ __forceinline__ float round_bf16(float x) { return __uint_as_float(f32_to_bf16_rne(x) << 16); }
-
 // ---------------------------------------------------------------------------
 // Vector path (path 1, on request): fp32 FMA instead of MFMA tiles, kept as a
 // second implementation the MFMA kernel is checked against. A wave owns VEC_RPW query rows; lane n

@@ -65,6 +65,16 @@ __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
   return u >> 16;
 }
 
+// Two fp32 values -> packed bf16 pair (low half = lo), round to nearest even
+// (v_cvt_pk_bf16_f32).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
+}
+// x rounded to the nearest bf16 value, as fp32.
+__device__ __forceinline__ float round_bf16(float x) { return bf16_lo(pack_bf16(x, 0.f)); }
+
 // Thread-local message for DKV_EINVAL returns.
 void set_error(const char* fmt, ...);
 void clear_error();

@@ -19,14 +19,6 @@
 namespace dkv {
 namespace {
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
-}
-__device__ __forceinline__ float round_bf16(float x) { return bf16_lo(pack_bf16(x, 0.f)); }
-
 __device__ __forceinline__ void unpack8(const uint4& w, float* x) {
   const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll

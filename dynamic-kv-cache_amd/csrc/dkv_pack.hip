@@ -67,23 +67,47 @@ __device__ __forceinline__ RowDst row_dst(const dkv_pack_job& j, int kv, int hea
   return d;
 }
 
-// Quantizes 8 elements of a row whose (offset, scale) is (a, s) and 1/s ~ r.
+// Codes of 8 elements of a row whose (offset, scale) is (a, s), with r ~ 1/s,
+// packed: BITS 4 -> out[0] (element e in bits 4e..4e+3), BITS 8 -> out[0..1]
+// (element e in byte e). `fast` says r and every t below are finite.
+//
+// rint(t) comes from m = t + 2^23, which for 0 <= t < 2^22 rounds t to an
+// integer (round to nearest even, as rintf) and leaves it in the low mantissa
+// bits: byte 0 of m's bit pattern is the code. The group takes the exact
+// division when any t is within 2^-13 of a half-integer.
 template <int BITS>
-__device__ __forceinline__ void quantize8(const float* x, float a, float s, float r, float* q) {
+__device__ __forceinline__ void quantize8(const float* x, float a, float s, float r, bool fast, uint32_t* out) {
   constexpr float LEVELS = BITS == 4 ? 15.0f : 255.0f;
-  bool ok = true;
+  constexpr float MAGIC = 0x1p23f;
+  uint32_t y[8];
+  float dev = 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float t = (x[e] - a) * r;
-    q[e] = rintf(t);
-    ok = ok && fabsf(t - q[e]) < TIE_GUARD;  // false for non-finite t
+    const float t = __fmul_rn(x[e] - a, r);
+    const float m = __fadd_rn(t, MAGIC);
+    dev = fmaxf(dev, fabsf(t - (m - MAGIC)));
+    y[e] = __float_as_uint(m);
   }
-  if (!ok) {
+  if (!(fast && dev < TIE_GUARD)) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) q[e] = rintf(__fdiv_rn(x[e] - a, s));
+    for (int e = 0; e < 8; ++e)
+      y[e] = (uint32_t)__builtin_amdgcn_fmed3f(rintf(__fdiv_rn(x[e] - a, s)), 0.0f, LEVELS);
   }
+  if (BITS == 4) {
+    uint32_t p[4];  // byte 0 of p[i] = element 2i + 1 in the high nibble, 2i in the low one
 #pragma unroll
-  for (int e = 0; e < 8; ++e) q[e] = __builtin_amdgcn_fmed3f(q[e], 0.0f, LEVELS);
+    for (int i = 0; i < 4; ++i) p[i] = (y[2 * i + 1] << 4) | y[2 * i];
+    const uint32_t lo = __builtin_amdgcn_perm(p[1], p[0], 0x07060400u);
+    const uint32_t hi = __builtin_amdgcn_perm(p[3], p[2], 0x07060400u);
+    out[0] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+  } else {
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      const uint32_t lo = __builtin_amdgcn_perm(y[4 * w + 1], y[4 * w], 0x07060400u);
+      const uint32_t hi = __builtin_amdgcn_perm(y[4 * w + 3], y[4 * w + 2], 0x07060400u);
+      out[w] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+    }
+  }
 }
 
 // A wave packs 64 rows (one per lane) staged through LDS: lanes load and store
@@ -95,15 +119,19 @@ __device__ __forceinline__ void quantize8(const float* x, float a, float s, floa
 constexpr int LROW = 144;                  // padded LDS row, bytes
 constexpr int WAVE_LDS = WAVE_ROWS * LROW;  // 9216 bytes per wave
 
+__device__ __forceinline__ void wave_sync_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Packs rows [tok0, tok0 + nrows) of the job's (kv, head) from registers: lane
+// l holds columns [8c, 8c + 8) (c = l & 7) of rows 8i + (l >> 3) in w[i].
 template <int BITS>
-__device__ __forceinline__ void pack_wave(const dkv_pack_job& j, int kv, int head, int tok0, uint8_t* arena,
-                                          int layers, int heads, uint8_t* lds) {
+__device__ __forceinline__ void pack_loaded(const dkv_pack_job& j, int kv, int head, int tok0, int nrows,
+                                            const u32x4* w, uint8_t* arena, int layers, int heads, uint8_t* lds) {
   const int lane = threadIdx.x & 63;
   const int c = lane & 7;
-  const uint16_t* base = kv == 0 ? static_cast<const uint16_t*>(j.k) + head * j.k_head_stride
-                                 : static_cast<const uint16_t*>(j.v) + head * j.v_head_stride;
-  const int64_t ts = kv == 0 ? j.k_tok_stride : j.v_tok_stride;
-  const int nrows = min(WAVE_ROWS, j.n - tok0);
   // Destination: one wave-uniform sub-block base when the wave's rows sit in
   // one tile (every append that starts on a tile boundary).
   const int rfirst = j.row0 + tok0;
@@ -111,14 +139,6 @@ __device__ __forceinline__ void pack_wave(const dkv_pack_job& j, int kv, int hea
   const bool one_tile = rfirst / TILE == rlast / TILE;
   const RowDst d0 = row_dst(j, kv, head, tok0, arena, layers, heads);
   constexpr int RB = BITS == 4 ? 32 : (BITS == 8 ? 64 : 128);
-
-  u32x4 w[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int r = 8 * i + (lane >> 3);
-    w[i] = r < nrows ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + (tok0 + r) * ts + 8 * c))
-                     : u32x4{0, 0, 0, 0};
-  }
   if (BITS == 16) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -132,9 +152,7 @@ __device__ __forceinline__ void pack_wave(const dkv_pack_job& j, int kv, int hea
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     *reinterpret_cast<u32x4*>(lds + (8 * i + (lane >> 3)) * LROW + 16 * c) = w[i];
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  wave_sync_lds();
   float x[64];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -153,27 +171,10 @@ __device__ __forceinline__ void pack_wave(const dkv_pack_job& j, int kv, int hea
   const float span = hi - a;
   const float s = span > 0.0f ? __fdiv_rn(span, BITS == 4 ? 15.0f : 255.0f) : 1.0f;
   const float rs = __builtin_amdgcn_rcpf(s);
+  const bool fast = s >= 0x1p-126f && s <= 0x1p125f;  // rs normal, every t finite and below 2^22
   uint32_t out[RB / 4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float q[8];
-    quantize8<BITS>(x + 8 * i, a, s, rs, q);
-    if (BITS == 4) {
-      uint32_t word = 0;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) word |= (uint32_t)q[e] << (4 * e);
-      out[i] = word;
-    } else {
-      uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        w0 |= (uint32_t)q[e] << (8 * e);
-        w1 |= (uint32_t)q[4 + e] << (8 * e);
-      }
-      out[2 * i] = w0;
-      out[2 * i + 1] = w1;
-    }
-  }
+  for (int i = 0; i < 8; ++i) quantize8<BITS>(x + 8 * i, a, s, rs, fast, out + (BITS == 4 ? i : 2 * i));
   const bool valid = lane < nrows;
   if (!one_tile) {  // rows straddle a tile boundary: each lane stores its own row
     if (valid) {
@@ -188,15 +189,11 @@ __device__ __forceinline__ void pack_wave(const dkv_pack_job& j, int kv, int hea
   if (valid) d0.meta[lane] = make_float2(a, s);
   // Packed rows back through LDS (the wave's own region, already read), then
   // contiguous 16-byte stores: RB bytes per row, rows back to back.
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  wave_sync_lds();
 #pragma unroll
   for (int i = 0; i < RB / 16; ++i)
     *reinterpret_cast<u32x4*>(lds + lane * RB + 16 * i) = u32x4{out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]};
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  wave_sync_lds();
   const int bytes = nrows * RB;
 #pragma unroll
   for (int i = 0; i < RB / 16; ++i) {
@@ -204,6 +201,25 @@ __device__ __forceinline__ void pack_wave(const dkv_pack_job& j, int kv, int hea
     if (off < bytes)
       *reinterpret_cast<u32x4*>(d0.payload + off) = *reinterpret_cast<const u32x4*>(lds + off);
   }
+}
+
+template <int BITS>
+__device__ __forceinline__ void pack_wave(const dkv_pack_job& j, int kv, int head, int tok0, uint8_t* arena,
+                                          int layers, int heads, uint8_t* lds) {
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 7;
+  const uint16_t* base = kv == 0 ? static_cast<const uint16_t*>(j.k) + head * j.k_head_stride
+                                 : static_cast<const uint16_t*>(j.v) + head * j.v_head_stride;
+  const int64_t ts = kv == 0 ? j.k_tok_stride : j.v_tok_stride;
+  const int nrows = min(WAVE_ROWS, j.n - tok0);
+  u32x4 w[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = 8 * i + (lane >> 3);
+    w[i] = r < nrows ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + (tok0 + r) * ts + 8 * c))
+                     : u32x4{0, 0, 0, 0};
+  }
+  pack_loaded<BITS>(j, kv, head, tok0, nrows, w, arena, layers, heads, lds);
 }
 
 __device__ __forceinline__ void write_segment_tiles(const dkv_pack_job& j, int layers, int heads,
@@ -249,6 +265,105 @@ pack_batch_kernel(const dkv_pack_job* __restrict__ jobs, int n_jobs, int wpj, ui
   const int wave = gw - ji * wpj;
   if (j.write_tiles && wave == 0) write_segment_tiles(j, layers, heads, tiles);
   pack_job_wave(j, wave, arena, layers, heads);
+}
+
+// Eight elements of one row after RoPE: y = bf16(bf16(x * cos) + bf16(sign *
+// partner * sin)), where partner is the element 32 columns away (rotate_half)
+// and sign is -1 on the first half of the row. Products of two bf16 values are
+// exact in fp32, so this is transformers' apply_rotary_pos_emb in bf16
+// operation by operation (q * cos + rotate_half(q) * sin, each op rounded).
+__device__ __forceinline__ u32x4 rope8(const u32x4& x, const u32x4& partner, const u32x4& cs, const u32x4& sn,
+                                       bool first_half) {
+  const float sg = first_half ? -1.0f : 1.0f;
+  u32x4 y;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float lo = round_bf16(round_bf16(bf16_lo(x[k]) * bf16_lo(cs[k])) +
+                                round_bf16(sg * bf16_lo(partner[k]) * bf16_lo(sn[k])));
+    const float hi = round_bf16(round_bf16(bf16_hi(x[k]) * bf16_hi(cs[k])) +
+                                round_bf16(sg * bf16_hi(partner[k]) * bf16_hi(sn[k])));
+    y[k] = pack_bf16(lo, hi);
+  }
+  return y;
+}
+
+// Joined Q/K/V projection rows -> RoPE -> q, k, v ([heads, n, 64] each) with K
+// and V also packed into the job's segment: the projection split,
+// apply_rotary_pos_emb and GPUCache.append of the patched attention forward
+// (src/gpu_cache.py:164-172) in one launch. One wave per (projection head,
+// 64-token slice): heads [0, q_heads) are Q, then `heads` K heads (rotated,
+// packed), then `heads` V heads (packed). The packed bytes come from the same
+// pack_loaded as dkv_pack on the same bf16 rows, so they are identical to a
+// RoPE launch followed by dkv_pack. With DEVJOB the job is read from device
+// memory when the kernel runs (HIP graph replays); the projection, not the
+// job's k/v pointers, is the source.
+template <bool DEVJOB>
+__global__ void __launch_bounds__(PACK_THREADS)
+rope_pack_kernel(const uint16_t* __restrict__ qkv, int64_t qkv_stride, const uint16_t* __restrict__ cosv,
+                 const uint16_t* __restrict__ sinv, int64_t cs_stride, int n, int q_heads,
+                 uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_out, uint16_t* __restrict__ v_out,
+                 dkv_pack_job hjob, const dkv_pack_job* __restrict__ djob, uint8_t* arena, dkv_tile* tiles,
+                 int layers, int heads) {
+  __shared__ __attribute__((aligned(16))) uint8_t stage[PACK_THREADS / 64][WAVE_LDS];
+  uint8_t* lds = stage[threadIdx.x >> 6];
+  const int gw = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * (PACK_THREADS / 64) + (threadIdx.x >> 6)));
+  const int slices = (n + WAVE_ROWS - 1) / WAVE_ROWS;
+  const int hh = gw / slices;
+  if (hh >= q_heads + 2 * heads) return;
+  const int tok0 = (gw - hh * slices) * WAVE_ROWS;
+  const int nrows = min(WAVE_ROWS, n - tok0);
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 7;
+  const bool is_v = hh >= q_heads + heads;
+
+  u32x4 w[8], cs[8], sn[8];
+  const uint16_t* src = qkv + hh * D + 8 * c;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = 8 * i + (lane >> 3);
+    w[i] = r < nrows ? *reinterpret_cast<const u32x4*>(src + (tok0 + r) * qkv_stride) : u32x4{0, 0, 0, 0};
+  }
+  if (!is_v) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = 8 * i + (lane >> 3);
+      const int64_t o = (int64_t)(tok0 + r) * cs_stride + 8 * c;
+      cs[i] = r < nrows ? *reinterpret_cast<const u32x4*>(cosv + o) : u32x4{0, 0, 0, 0};
+      sn[i] = r < nrows ? *reinterpret_cast<const u32x4*>(sinv + o) : u32x4{0, 0, 0, 0};
+    }
+    // rotate_half pairs column d with d +- 32, i.e. lane c with lane c ^ 4 of
+    // the same row: exchange through the wave's LDS region.
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      *reinterpret_cast<u32x4*>(lds + (8 * i + (lane >> 3)) * LROW + 16 * c) = w[i];
+    wave_sync_lds();
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const u32x4 p = *reinterpret_cast<const u32x4*>(lds + (8 * i + (lane >> 3)) * LROW + 16 * (c ^ 4));
+      w[i] = rope8(w[i], p, cs[i], sn[i], c < 4);
+    }
+    wave_sync_lds();  // every lane has read its partner before the region is reused
+  }
+  uint16_t* dst = hh < q_heads ? q_out + (int64_t)hh * n * D
+                               : (is_v ? v_out + (int64_t)(hh - q_heads - heads) * n * D
+                                       : k_out + (int64_t)(hh - q_heads) * n * D);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = 8 * i + (lane >> 3);
+    if (r < nrows) *reinterpret_cast<u32x4*>(dst + (int64_t)(tok0 + r) * D + 8 * c) = w[i];
+  }
+
+  const dkv_pack_job j = DEVJOB ? *djob : hjob;
+  if (gw == 0 && j.write_tiles) write_segment_tiles(j, layers, heads, tiles);
+  if (hh < q_heads) return;
+  const int np = min(WAVE_ROWS, min(j.n, n) - tok0);  // rows of this slice the job packs
+  if (np <= 0) return;
+  const int kv = is_v ? 1 : 0;
+  const int head = hh - q_heads - kv * heads;
+  const int bits = __builtin_amdgcn_readfirstlane(j.bits);
+  if (bits == 4) pack_loaded<4>(j, kv, head, tok0, np, w, arena, layers, heads, lds);
+  else if (bits == 8) pack_loaded<8>(j, kv, head, tok0, np, w, arena, layers, heads, lds);
+  else pack_loaded<16>(j, kv, head, tok0, np, w, arena, layers, heads, lds);
 }
 
 static int pack_waves(int n, int heads) { return 2 * heads * ((n + WAVE_ROWS - 1) / WAVE_ROWS); }
@@ -398,6 +513,60 @@ int dkv_pack_batch(const dkv_pack_job* jobs, int32_t n_jobs, int32_t max_n, void
   const int64_t blocks = ((int64_t)n_jobs * wpj + PACK_THREADS / 64 - 1) / (PACK_THREADS / 64);
   hipLaunchKernelGGL(pack_batch_kernel, dim3((unsigned)blocks), dim3(PACK_THREADS), 0, (hipStream_t)stream, jobs,
                      n_jobs, wpj, static_cast<uint8_t*>(arena), tiles, layers, heads);
+  return (int)hipGetLastError();
+}
+
+int dkv_rope_pack(const void* qkv, int64_t qkv_row_stride, const void* cos, const void* sin, int64_t cs_row_stride,
+                  int32_t n, int32_t q_heads, void* q_out, void* k_out, void* v_out, const dkv_pack_job* job,
+                  int32_t job_on_device, void* arena, int64_t arena_bytes, dkv_tile* tiles, int32_t layers,
+                  int32_t heads, void* stream) {
+  clear_error();
+  if (!qkv || !cos || !sin || !q_out || !k_out || !v_out || !job || !arena || !tiles || n < 0 || q_heads <= 0 ||
+      heads <= 0 || layers <= 0 || !aligned16(qkv) || !aligned16(cos) || !aligned16(sin) || !aligned16(q_out) ||
+      !aligned16(k_out) || !aligned16(v_out) || (qkv_row_stride & 7) || (cs_row_stride & 7) ||
+      qkv_row_stride < (int64_t)(q_heads + 2 * heads) * D || cs_row_stride < D) {
+    set_error("dkv_rope_pack: bad arguments (16-byte aligned bf16 buffers, strides multiples of 8 elements)");
+    return DKV_EINVAL;
+  }
+  if (job_on_device) {
+    if (n < 1) {
+      set_error("dkv_rope_pack: a device job needs a chunk of at least one token");
+      return DKV_EINVAL;
+    }
+  } else {
+    if (int rc = check_job(*job, arena_bytes, layers, heads)) return rc;
+    if (job->n != n) {
+      set_error("dkv_rope_pack: the job appends %d tokens, the projection holds %d", job->n, n);
+      return DKV_EINVAL;
+    }
+    if (job->write_tiles && job->tile_index0 < 0) {
+      set_error("dkv_rope_pack: write_tiles at a negative tile index");
+      return DKV_EINVAL;
+    }
+  }
+  if (n == 0) {  // nothing to rotate; the append may still open a segment
+    if (!job->write_tiles) return 0;
+    hipLaunchKernelGGL(pack_one_kernel, dim3(1), dim3(PACK_THREADS), 0, (hipStream_t)stream, *job,
+                       static_cast<uint8_t*>(arena), tiles, layers, heads);
+    return (int)hipGetLastError();
+  }
+  const int64_t waves = (int64_t)(q_heads + 2 * heads) * ((n + WAVE_ROWS - 1) / WAVE_ROWS);
+  const unsigned blocks = (unsigned)((waves + PACK_THREADS / 64 - 1) / (PACK_THREADS / 64));
+  const dkv_pack_job none = {};
+  const auto* qp = static_cast<const uint16_t*>(qkv);
+  const auto* cp = static_cast<const uint16_t*>(cos);
+  const auto* sp = static_cast<const uint16_t*>(sin);
+  auto* qo = static_cast<uint16_t*>(q_out);
+  auto* ko = static_cast<uint16_t*>(k_out);
+  auto* vo = static_cast<uint16_t*>(v_out);
+  if (job_on_device)
+    hipLaunchKernelGGL(rope_pack_kernel<true>, dim3(blocks), dim3(PACK_THREADS), 0, (hipStream_t)stream, qp,
+                       qkv_row_stride, cp, sp, cs_row_stride, n, q_heads, qo, ko, vo, none, job,
+                       static_cast<uint8_t*>(arena), tiles, layers, heads);
+  else
+    hipLaunchKernelGGL(rope_pack_kernel<false>, dim3(blocks), dim3(PACK_THREADS), 0, (hipStream_t)stream, qp,
+                       qkv_row_stride, cp, sp, cs_row_stride, n, q_heads, qo, ko, vo, *job,
+                       (const dkv_pack_job*)nullptr, static_cast<uint8_t*>(arena), tiles, layers, heads);
   return (int)hipGetLastError();
 }
 

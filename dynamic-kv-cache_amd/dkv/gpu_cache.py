@@ -227,8 +227,22 @@ class GPUCache(_CacheBase):
             raise ValueError(f'append expects k and v of shape [1, {self.heads}, n, {self.dim}]')
         if self._graph is not None:
             return self._graph.append(k, v, layer)
-        past = self.seen[layer]
         n = k.shape[-2]
+        past, seg, write_tiles = self._claim(layer, n)
+        if n:
+            k, v = self._kv_view(k), self._kv_view(v)
+            job = self._job(k, v, layer, past, n, seg, write_tiles)
+            lib = _lib.load()
+            _lib.check(lib.dkv_pack(ctypes.byref(job), self.arena.data_ptr(), self.arena_bytes,
+                                    self.tiles.data_ptr(), self.layers, self.heads,
+                                    _lib.stream_handle(self.device)), 'dkv_pack')
+        self.seen[layer] = past + n
+        return past
+
+    def _claim(self, layer, n):
+        """Bookkeeping of an append of n tokens to `layer` (src/gpu_cache.py:70-88): the segment the
+        tokens go to, opened on layer 0 in online mode. Returns (past, segment, write_tiles)."""
+        past = self.seen[layer]
         if past + n > self.capacity:
             raise ValueError('GPU context limit exceeded')
         write_tiles = 0
@@ -248,17 +262,47 @@ class GPUCache(_CacheBase):
                 seg.frame = self.frame_id
         if seg is None or past + n > seg.end or seg.bits != self.pending_bits:
             raise ValueError(f'Cache append does not match plan at token {past}, length {n}, bits {self.pending_bits}')
-        if n:
-            k, v = self._kv_view(k), self._kv_view(v)
-            job = _lib.PackJob(k.data_ptr(), v.data_ptr(), k.stride(1), k.stride(2), v.stride(1), v.stride(2),
-                               seg.offset, seg.rows, seg.start, past - seg.start, n, layer, seg.bits,
-                               seg.tile0, write_tiles)
-            lib = _lib.load()
-            _lib.check(lib.dkv_pack(ctypes.byref(job), self.arena.data_ptr(), self.arena_bytes,
-                                    self.tiles.data_ptr(), self.layers, self.heads,
-                                    _lib.stream_handle(self.device)), 'dkv_pack')
+        return past, seg, write_tiles
+
+    @staticmethod
+    def _job(k, v, layer, past, n, seg, write_tiles):
+        return _lib.PackJob(k.data_ptr(), v.data_ptr(), k.stride(1), k.stride(2), v.stride(1), v.stride(2),
+                            seg.offset, seg.rows, seg.start, past - seg.start, n, layer, seg.bits, seg.tile0,
+                            write_tiles)
+
+    def append_projection(self, qkv, cos, sin, q_heads, layer):
+        """The joined Q/K/V projection of one layer -> (q, k, v, past), with RoPE on q and k and the
+        new K/V packed, in one launch (dkv_rope_pack).
+
+        Equivalent to splitting qkv [1, n, (q_heads + 2 heads) * 64], applying transformers'
+        apply_rotary_pos_emb with cos/sin [1, n, 64] and calling append(k, v, layer), as the patched
+        attention forward does (src/gpu_cache.py:164-172): q [1, q_heads, n, 64] and k, v
+        [1, heads, n, 64] are bit-equal to that path and the packed bytes identical. Returns None
+        when the inputs are outside what the kernel covers (the caller then takes that path).
+        """
+        n = qkv.shape[1] if qkv.dim() == 3 else -1
+        if (n < 1 or qkv.shape[0] != 1 or qkv.shape[2] != (q_heads + 2 * self.heads) * self.dim
+                or self.dim != 64 or cos.shape[-2:] != (n, 64) or sin.shape != cos.shape
+                or not all(t.is_cuda and t.dtype == torch.bfloat16 for t in (qkv, cos, sin))):
+            return None
+        qkv2, cos2, sin2 = qkv.reshape(n, -1), cos.reshape(n, 64), sin.reshape(n, 64)
+        if any(t.stride(-1) != 1 or t.stride(0) % 8 or t.data_ptr() % 16 for t in (qkv2, cos2, sin2)):
+            return None
+        q = torch.empty((1, q_heads, n, 64), dtype=qkv.dtype, device=qkv.device)
+        k = torch.empty((1, self.heads, n, 64), dtype=qkv.dtype, device=qkv.device)
+        v = torch.empty_like(k)
+        if self._graph is not None:
+            past = self._graph.append_projection(qkv2, cos2, sin2, q_heads, layer, q, k, v)
+            return q, k, v, past
+        past, seg, write_tiles = self._claim(layer, n)
+        job = self._job(k, v, layer, past, n, seg, write_tiles)
+        _lib.check(_lib.load().dkv_rope_pack(
+            qkv2.data_ptr(), qkv2.stride(0), cos2.data_ptr(), sin2.data_ptr(), cos2.stride(0), n, q_heads,
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), ctypes.byref(job), 0, self.arena.data_ptr(),
+            self.arena_bytes, self.tiles.data_ptr(), self.layers, self.heads, _lib.stream_handle(self.device)),
+            'dkv_rope_pack')
         self.seen[layer] = past + n
-        return past
+        return q, k, v, past
 
     def append_batch(self, k, v, bits, lengths):
         """Appends several segments for every layer in one pack launch.
@@ -585,8 +629,10 @@ class GraphSteps:
         self.cache, self.chunk = cache, chunk
         self.job_bytes = ctypes.sizeof(_lib.PackJob)
         self.nbytes = cache.layers * self.job_bytes + 8
-        self.dev = torch.zeros(self.nbytes, dtype=torch.uint8, device=cache.device)
-        self.ring = [(torch.zeros(self.nbytes, dtype=torch.uint8, pin_memory=True), None) for _ in range(self.RING)]
+        with torch.inference_mode(False):  # ordinary tensors: step() may run inside or outside inference mode
+            self.dev = torch.zeros(self.nbytes, dtype=torch.uint8, device=cache.device)
+            self.ring = [(torch.zeros(self.nbytes, dtype=torch.uint8, pin_memory=True), None)
+                         for _ in range(self.RING)]
         self.slot = 0
         self.kv = [None] * cache.layers  # (k, v) views append() recorded, kept alive with the graph
         self.state = None  # (past, segment, write_tiles) of the current step
@@ -653,6 +699,20 @@ class GraphSteps:
         _lib.check(_lib.load().dkv_pack_batch(self.dev.data_ptr() + layer * self.job_bytes, 1, self.chunk,
                                               c.arena.data_ptr(), c.arena_bytes, c.tiles.data_ptr(), c.layers,
                                               c.heads, _lib.stream_handle(c.device)), 'dkv_pack_batch')
+        return self.state[0]
+
+    def append_projection(self, qkv, cos, sin, q_heads, layer, q, k, v):
+        c = self.cache
+        if self.state is None:
+            raise ValueError('graph_step() must run before the recorded append')
+        if qkv.shape[0] != self.chunk:
+            raise ValueError(f'graph steps were set up for {self.chunk}-token chunks, got {qkv.shape[0]}')
+        self.kv[layer] = (k, v)
+        _lib.check(_lib.load().dkv_rope_pack(
+            qkv.data_ptr(), qkv.stride(0), cos.data_ptr(), sin.data_ptr(), cos.stride(0), self.chunk, q_heads,
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), self.dev.data_ptr() + layer * self.job_bytes, 1,
+            c.arena.data_ptr(), c.arena_bytes, c.tiles.data_ptr(), c.layers, c.heads,
+            _lib.stream_handle(c.device)), 'dkv_rope_pack')
         return self.state[0]
 
     def attend_args(self, q, k, v, layer, out, segments, path, splits, precision):
@@ -799,8 +859,17 @@ def install_packed_attention(model):
         if fused and hasattr(module, '_qkv_weight'):
             qkv = F.linear(hidden_states, module._qkv_weight)
             hd = module.head_dim
-            # split + RoPE in one launch (bit-equal to apply_rotary_pos_emb in bf16)
-            roped = rope_qkv(qkv, *position_embeddings, module._qkv_sizes[0] // hd, module._qkv_sizes[1] // hd, hd)
+            nq, nkv = module._qkv_sizes[0] // hd, module._qkv_sizes[1] // hd
+            if nkv == cache.heads:
+                # split + RoPE + append in one launch (bit-equal to apply_rotary_pos_emb in bf16
+                # followed by append)
+                packed = cache.append_projection(qkv, *position_embeddings, nq, module.layer_idx)
+                if packed is not None:
+                    q, k, v, past = packed
+                    output = cache.attend(q, k, v, module.layer_idx, past)
+                    return module.o_proj(output.reshape(*shape, -1).contiguous()), None
+            # split + RoPE in one launch
+            roped = rope_qkv(qkv, *position_embeddings, nq, nkv, hd)
             if roped is None:
                 q, k, v = qkv.split(module._qkv_sizes, dim=-1)
         else:

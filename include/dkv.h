@@ -218,6 +218,22 @@ int dkv_rope_qkv(const void* qkv, int64_t qkv_row_stride, const void* cos, const
                  int64_t cs_row_stride, int32_t n, int32_t q_heads, int32_t kv_heads,
                  void* q_out, void* k_out, void* v_out, void* stream);
 
+/* dkv_rope_qkv and dkv_pack in one launch: the projection split, RoPE and the
+ * cache append of the reference's patched attention forward
+ * (src/gpu_cache.py:164-172, the append at src/gpu_cache.py:68-94). Writes
+ * q_out/k_out/v_out as dkv_rope_qkv does (kv_heads = heads) and packs k_out's
+ * and v_out's rows into the job's segment, byte for byte what dkv_pack of the
+ * same job over those outputs writes. The job's k/v pointers and strides are
+ * not read: the projection is the source. job_on_device = 0: `job` is a host
+ * struct, checked as dkv_pack checks it, and job->n must equal n.
+ * job_on_device = 1: `job` is a DEVICE struct read when the kernel runs (HIP
+ * graph replays; validate its host copy with dkv_pack_validate), n >= 1, and
+ * the kernel packs min(job->n, n) rows. */
+int dkv_rope_pack(const void* qkv, int64_t qkv_row_stride, const void* cos, const void* sin,
+                  int64_t cs_row_stride, int32_t n, int32_t q_heads, void* q_out, void* k_out,
+                  void* v_out, const dkv_pack_job* job, int32_t job_on_device, void* arena,
+                  int64_t arena_bytes, dkv_tile* tiles, int32_t layers, int32_t heads, void* stream);
+
 /* out = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * weight) per row of `dim`
  * elements: the reference's cuda_rms (src/gpu_ops.py:9-12) in one launch. */
 int dkv_rms_norm(const void* x, int64_t x_row_stride, const void* weight, void* out,

@@ -232,3 +232,22 @@ def test_pointwise_ops_reject_misaligned_buffers():
     assert lib.dkv_silu_mul(ok, 4000, ok, 2560, 4, 2560, None) == _lib.DKV_EINVAL  # row holds < 2 * inter
     assert 'dkv_silu_mul' in lib.dkv_last_error().decode()
     assert lib.dkv_rms_norm(ok, 960, ok, ok, 960, 0, 960, 1e-5, None) == 0  # no rows: nothing to launch
+
+
+def test_rope_pack_rejects_bad_arguments_without_touching_the_device():
+    lib = _lib.load()
+    ok, bad = ctypes.c_void_p(4096), ctypes.c_void_p(4098)
+    arena = ctypes.c_void_p(1 << 16)
+
+    def call(qkv=ok, stride=1600, n=64, j=None, on_device=0):
+        j = job(n=64) if j is None else j
+        return lib.dkv_rope_pack(qkv, stride, ok, ok, 64, n, 15, ok, ok, ok, ctypes.byref(j), on_device, arena,
+                                 1 << 20, ok, 2, 5, None)
+
+    assert call(qkv=bad) == _lib.DKV_EINVAL
+    assert call(stride=1000) == _lib.DKV_EINVAL  # a row holds fewer than 25 heads
+    assert call(n=32) == _lib.DKV_EINVAL and 'projection holds' in lib.dkv_last_error().decode()
+    assert call(j=job(n=64, bits=5)) == _lib.DKV_EINVAL and 'bits' in lib.dkv_last_error().decode()
+    assert call(n=0, on_device=1) == _lib.DKV_EINVAL and 'device job' in lib.dkv_last_error().decode()
+    assert lib.dkv_rope_pack(ok, 1600, ok, ok, 64, 64, 15, ok, ok, ok, None, 0, arena, 1 << 20, ok, 2, 5,
+                             None) == _lib.DKV_EINVAL  # no job

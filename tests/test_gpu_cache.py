@@ -95,3 +95,22 @@ def test_candidate_forks_sequentially_reuse_the_qa_region(cuda):
             outs.append((past, b.attend(q, k, k, 0, past).clone()))
     assert all(p == 256 for p, _ in outs)
     assert c.get_seq_length() == 256 and len(c.segments) == 1
+
+
+def test_graph_steps_created_in_inference_mode_step_outside_it(cuda):
+    """GraphSteps' device and pinned buffers are ordinary tensors, so graph_step() works whether or
+    not the caller is in inference mode (no launch here: nothing was recorded)."""
+    announce('cache: graph steps across inference mode')
+    c = GPUCache(None, layers=2, heads=5, max_tokens=512)
+    with torch.inference_mode():
+        c.begin_graph_steps(64, q_heads=15)
+        c.select(4, 0)
+        assert c.graph_step() == 0
+    c.select(8, 1)
+    assert c.graph_step() == 64
+    with torch.inference_mode():
+        c.select(16, 2)
+        assert c.graph_step() == 128
+    c.end_graph_steps()
+    torch.cuda.synchronize()
+    assert c.seen == [192, 192] and [s.bits for s in c.segments] == [4, 8, 16]

@@ -56,8 +56,9 @@ def test_ties_constants_and_extremes(cuda):
     rows[3] = torch.linspace(-3e4, 3e4, 64)
     rows[4] = torch.tensor([1e-30 * i for i in range(64)])  # tiny span
     rows[5] = torch.tensor([1e-39 * i for i in range(64)])  # fp32 subnormal values and scale
+    rows[6] = torch.linspace(-1e38, 1e38, 64)  # span near the top of the fp32 range
     g = torch.Generator().manual_seed(4)
-    rows[6:] = torch.randn(58, 64, generator=g) * torch.logspace(-3, 3, 58)[:, None]
+    rows[7:] = torch.randn(57, 64, generator=g) * torch.logspace(-3, 3, 57)[:, None]
     x = rows.to(torch.bfloat16)
     for bits in (4, 8):
         c = GPUCache([(bits, 64)], layers=1, heads=1)
