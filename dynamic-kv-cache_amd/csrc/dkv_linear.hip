@@ -1,0 +1,345 @@
+// Decoder projections for short chunks: out = epilogue(prologue(x) w^T) with
+// x [rows, k] and w [n, k] bf16 (both row-major, k contiguous), fp32
+// accumulation on v_mfma_f32_16x16x32_bf16, bf16 out.
+//
+//   prologue  none, or RMSNorm of the x rows with the torch composition's two
+//             bf16 roundings (bf16(bf16(x * rsqrt(mean(x^2) + eps)) * g),
+//             src/gpu_ops.py:9-12) applied in registers;
+//   epilogue  plain: bf16(acc);
+//             residual: bf16(r + bf16(acc)), the decoder's residual add after
+//             o_proj and down_proj;
+//             silu_mul: w holds [gate | up] rows (2 * inter of them) and
+//             out[:, c] = bf16(bf16(silu(bf16(g_c))) * bf16(u_c))
+//             (src/gpu_ops.py:14-17, 23-25).
+//
+// The chunks are 1-100 rows, so the weights (1.8-9.8 MB per projection of the
+// 960-wide decoder) dominate the traffic: the kernel is a weight stream. A
+// workgroup owns NB column blocks of 16 weight rows and RB blocks of 16 x
+// rows; its waves split k in 64-element pairs of MFMA steps (wave w takes
+// pairs w, w + WAVES, ...), issue every load of their share before the first
+// MFMA, and meet in LDS, where one wave per output tile sums the partials in
+// wave order (deterministic). With Y^T = W X^T on the MFMA (weights on the M
+// axis), lane (col, g) ends with 4 consecutive output columns of one row: 8
+// byte stores. Consecutive workgroups go to different XCDs; the RB = 1 layout
+// numbers its tiles so that the row blocks sharing a weight tile land on one
+// XCD (one L2).
+#include "dkv_common.h"
+
+namespace dkv {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+union Op8 {
+  bf16x8_t v;
+  u32x4 u;
+};
+
+enum { EPI_PLAIN = 0, EPI_RESIDUAL = 1, EPI_SILU_MUL = 2 };
+
+struct LinearArgs {  // passed by value and never written (a written copy would go to scratch)
+  const uint16_t* x;
+  int64_t ldx;
+  const uint16_t* w;
+  int64_t ldw;
+  const uint16_t* norm;  // RMSNorm weight [k] (prologue only)
+  const uint16_t* res;   // residual [rows, n] (EPI_RESIDUAL only)
+  int64_t ldr;
+  uint16_t* out;
+  int64_t ldo;
+  float eps;
+  int rows, k, kp;  // kp = k / 64
+  int n_tiles;      // column tiles of 16 * NT output columns
+  int row_groups;   // ceil(rows / (16 * RB))
+  int up;           // EPI_SILU_MUL: first weight row of the up half (= inter)
+};
+
+__device__ __forceinline__ float lane_group_sum(float x) {
+  // sum over lanes col, col + 16, col + 32, col + 48 (gfx950 lane swaps)
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
+template <int CH, int NT, int WAVES, int RB, int EPI, bool NORM>
+__global__ void __launch_bounds__(64 * WAVES) linear_kernel(const LinearArgs a) {
+  constexpr int NB = EPI == EPI_SILU_MUL ? 2 * NT : NT;  // column blocks multiplied
+  const int b = blockIdx.x;
+  const int xcd = b & 7, j = b >> 3;
+  const int rg = j % a.row_groups;
+  const int ct = (j / a.row_groups) * 8 + xcd;
+  if (ct >= a.n_tiles) return;  // uniform over the workgroup
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, g = lane >> 4;
+  const int n0 = ct * 16 * NT;
+
+  const uint16_t* wrow[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int r = (EPI == EPI_SILU_MUL && nb >= NT) ? a.up + n0 + 16 * (nb - NT) + col : n0 + 16 * nb + col;
+    wrow[nb] = a.w + (int64_t)r * a.ldw + 8 * g;
+  }
+  const uint16_t* xrow[RB];
+  bool xin[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int row = (rg * RB + rb) * 16 + col;
+    xin[rb] = row < a.rows;
+    xrow[rb] = a.x + (int64_t)(xin[rb] ? row : 0) * a.ldx + 8 * g;
+  }
+
+  f32x4_t acc[RB][NB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[rb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  __shared__ float ssum[NORM ? WAVES : 1][RB][16];
+  const int per_wave = (a.kp + WAVES - 1) / WAVES;  // pairs of this wave (upper bound)
+  for (int c0 = 0; c0 < per_wave; c0 += CH) {
+    Op8 xa[CH][2][RB], wa[CH][2][NB];
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int p = wave + WAVES * (c0 + i);
+      if (p < a.kp) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int k = 64 * p + 32 * h;
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) wa[i][h][nb].u = *reinterpret_cast<const u32x4*>(wrow[nb] + k);
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb)
+            xa[i][h][rb].u = xin[rb] ? *reinterpret_cast<const u32x4*>(xrow[rb] + k) : u32x4{0, 0, 0, 0};
+        }
+      }
+    }
+    if (NORM) {  // the host guarantees one chunk (CH * WAVES >= kp): every wave holds all of its pairs
+      Op8 gn[CH][2];
+#pragma unroll
+      for (int i = 0; i < CH; ++i) {
+        const int p = wave + WAVES * (c0 + i);
+        if (p < a.kp)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            gn[i][h].u = *reinterpret_cast<const u32x4*>(a.norm + 64 * p + 32 * h + 8 * g);
+      }
+      float ss[RB];
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        ss[rb] = 0.f;
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+          if (wave + WAVES * (c0 + i) < a.kp)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const float lo = bf16_lo(xa[i][h][rb].u[e]), hi = bf16_hi(xa[i][h][rb].u[e]);
+                ss[rb] = __fmaf_rn(lo, lo, ss[rb]);
+                ss[rb] = __fmaf_rn(hi, hi, ss[rb]);
+              }
+        }
+        ss[rb] = lane_group_sum(ss[rb]);
+        if (g == 0) ssum[wave][rb][col] = ss[rb];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        float tot = 0.f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) tot += ssum[w][rb][col];
+        const float rstd = 1.f / sqrtf(tot / (float)a.k + a.eps);
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+          if (wave + WAVES * (c0 + i) < a.kp)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const uint32_t xv = xa[i][h][rb].u[e], gv = gn[i][h].u[e];
+                xa[i][h][rb].u[e] = pack_bf16(round_bf16(bf16_lo(xv) * rstd) * bf16_lo(gv),
+                                              round_bf16(bf16_hi(xv) * rstd) * bf16_hi(gv));
+              }
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      if (wave + WAVES * (c0 + i) < a.kp)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+              acc[rb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[i][h][nb].v, xa[i][h][rb].v, acc[rb][nb], 0, 0, 0);
+    }
+  }
+
+  // Every wave stores its partials; one wave per output tile adds them up in
+  // wave order.
+  __shared__ f32x4_t red[WAVES][RB * NB][64];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) red[wave][rb * NB + nb][lane] = acc[rb][nb];
+  __syncthreads();
+  auto tile_sum = [&](int rb, int nb) {
+    f32x4_t s = red[0][rb * NB + nb][lane];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) {
+      const f32x4_t v = red[w][rb * NB + nb][lane];
+      s[0] += v[0];
+      s[1] += v[1];
+      s[2] += v[2];
+      s[3] += v[3];
+    }
+    return s;
+  };
+  for (int t = wave; t < RB * NT; t += WAVES) {
+    const int rb = t / NT, nt = t - rb * NT;
+    const f32x4_t s = tile_sum(rb, nt);
+    const int row = (rg * RB + rb) * 16 + col;
+    if (row >= a.rows) continue;
+    const int c = n0 + 16 * nt + 4 * g;
+    float y[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) y[e] = round_bf16(s[e]);
+    if (EPI == EPI_RESIDUAL) {
+      const uint2 r = *reinterpret_cast<const uint2*>(a.res + (int64_t)row * a.ldr + c);
+      y[0] += bf16_lo(r.x);
+      y[1] += bf16_hi(r.x);
+      y[2] += bf16_lo(r.y);
+      y[3] += bf16_hi(r.y);
+    } else if (EPI == EPI_SILU_MUL) {
+      const f32x4_t u = tile_sum(rb, NT + nt);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] = round_bf16(y[e] / (1.f + expf(-y[e]))) * round_bf16(u[e]);
+    }
+    *reinterpret_cast<uint2*>(a.out + (int64_t)row * a.ldo + c) = make_uint2(pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3]));
+  }
+}
+
+bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// Launch shapes, from graph-replay timings of the 960-wide decoder's projections at 64 rows
+// (weights streamed from HBM): narrow outputs use one 16-row block per workgroup (more
+// workgroups), the joined gate/up projection 32 rows (each weight tile read twice per 64 rows).
+struct Shape {
+  int ch, nt, waves, rb;
+};
+
+constexpr int MAX_CH = 5;       // pairs per wave and chunk
+constexpr int MAX_NORM_CH = 2;  // with the RMSNorm prologue a row's pairs must fit one chunk
+                                // (k <= 1024), which also keeps those variants out of scratch
+
+Shape pick(int n_out, int kp, int epilogue) {
+  Shape s;
+  s.waves = 8;
+  if (epilogue == EPI_SILU_MUL) {  // gate and up blocks: two weight tiles per workgroup
+    s.nt = 1;
+    s.rb = 2;
+  } else {
+    s.nt = (n_out % 32 == 0 && n_out / 16 > 64) ? 2 : 1;
+    s.rb = 1;
+  }
+  const int per = (kp + s.waves - 1) / s.waves;
+  s.ch = per <= MAX_CH ? per : 4;
+  return s;
+}
+
+template <int CH, int NT, int WAVES, int RB, int EPI, bool NORM>
+void launch_one(const LinearArgs& a, hipStream_t st) {
+  const int groups = (a.n_tiles + 7) / 8;
+  const unsigned blocks = (unsigned)groups * 8u * (unsigned)a.row_groups;
+  hipLaunchKernelGGL((linear_kernel<CH, NT, WAVES, RB, EPI, NORM>), dim3(blocks), dim3(64 * WAVES), 0, st, a);
+}
+
+template <int NT, int WAVES, int RB, int EPI, bool NORM>
+void launch_ch(int ch, const LinearArgs& a, hipStream_t st) {
+  if constexpr (NORM) {
+    if (ch == 1) launch_one<1, NT, WAVES, RB, EPI, NORM>(a, st);
+    else launch_one<MAX_NORM_CH, NT, WAVES, RB, EPI, NORM>(a, st);
+  } else {
+    switch (ch) {
+      case 1: launch_one<1, NT, WAVES, RB, EPI, NORM>(a, st); break;
+      case 2: launch_one<2, NT, WAVES, RB, EPI, NORM>(a, st); break;
+      case 3: launch_one<3, NT, WAVES, RB, EPI, NORM>(a, st); break;
+      case 4: launch_one<4, NT, WAVES, RB, EPI, NORM>(a, st); break;
+      default: launch_one<MAX_CH, NT, WAVES, RB, EPI, NORM>(a, st); break;
+    }
+  }
+}
+
+template <int EPI, bool NORM>
+void launch_epi(const Shape& s, const LinearArgs& a, hipStream_t st) {
+  if constexpr (EPI == EPI_SILU_MUL) {
+    launch_ch<1, 8, 2, EPI, NORM>(s.ch, a, st);
+  } else {
+    if (s.nt == 2) launch_ch<2, 8, 1, EPI, NORM>(s.ch, a, st);
+    else launch_ch<1, 8, 1, EPI, NORM>(s.ch, a, st);
+  }
+}
+
+}  // namespace
+}  // namespace dkv
+
+using namespace dkv;
+
+extern "C" {
+
+int dkv_linear_supported(int32_t rows, int32_t n, int32_t k, int32_t has_norm, int32_t epilogue) {
+  if (rows < 0 || n <= 0 || k <= 0 || (k & 63) || epilogue < 0 || epilogue > 2) return 0;
+  const int n_out = epilogue == EPI_SILU_MUL ? n / 2 : n;
+  if (epilogue == EPI_SILU_MUL && (n & 1)) return 0;
+  if (n_out % 16) return 0;
+  const Shape s = pick(n_out, k / 64, epilogue);
+  if (has_norm && (s.ch > MAX_NORM_CH || s.ch * s.waves < k / 64)) return 0;  // a row's pairs in one chunk
+  if (s.nt == 2 && n_out % 32) return 0;
+  return 1;
+}
+
+int dkv_linear(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride, int32_t rows, int32_t n,
+               int32_t k, const void* norm_weight, float eps, int32_t epilogue, const void* residual,
+               int64_t residual_row_stride, void* out, int64_t out_row_stride, void* stream) {
+  clear_error();
+  const bool norm = norm_weight != nullptr;
+  const int n_out = epilogue == EPI_SILU_MUL ? n / 2 : n;
+  if (!x || !w || !out || !dkv_linear_supported(rows, n, k, norm, epilogue) || !al16(x) || !al16(w) ||
+      !al16(out) || (norm && !al16(norm_weight)) || (x_row_stride & 7) || (w_row_stride & 7) ||
+      (out_row_stride & 3) || x_row_stride < k || w_row_stride < k || out_row_stride < n_out ||
+      (epilogue == EPI_RESIDUAL &&
+       (!residual || ((uintptr_t)residual & 7) || (residual_row_stride & 3) || residual_row_stride < n_out))) {
+    set_error("dkv_linear: unsupported or bad arguments (rows %d, n %d, k %d, epilogue %d; k a multiple of 64, "
+              "16-byte aligned bf16 rows)", rows, n, k, epilogue);
+    return DKV_EINVAL;
+  }
+  if (rows == 0) return 0;
+  const Shape s = pick(n_out, k / 64, epilogue);
+  LinearArgs a;
+  a.x = static_cast<const uint16_t*>(x);
+  a.ldx = x_row_stride;
+  a.w = static_cast<const uint16_t*>(w);
+  a.ldw = w_row_stride;
+  a.norm = static_cast<const uint16_t*>(norm_weight);
+  a.res = static_cast<const uint16_t*>(residual);
+  a.ldr = residual_row_stride;
+  a.out = static_cast<uint16_t*>(out);
+  a.ldo = out_row_stride;
+  a.eps = eps;
+  a.rows = rows;
+  a.k = k;
+  a.kp = k / 64;
+  a.n_tiles = n_out / (16 * s.nt);
+  a.row_groups = (rows + 16 * s.rb - 1) / (16 * s.rb);
+  a.up = n_out;
+  hipStream_t st = (hipStream_t)stream;
+  if (epilogue == EPI_PLAIN) norm ? launch_epi<EPI_PLAIN, true>(s, a, st) : launch_epi<EPI_PLAIN, false>(s, a, st);
+  else if (epilogue == EPI_RESIDUAL)
+    norm ? launch_epi<EPI_RESIDUAL, true>(s, a, st) : launch_epi<EPI_RESIDUAL, false>(s, a, st);
+  else norm ? launch_epi<EPI_SILU_MUL, true>(s, a, st) : launch_epi<EPI_SILU_MUL, false>(s, a, st);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"

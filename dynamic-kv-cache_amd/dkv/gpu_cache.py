@@ -832,6 +832,33 @@ class PackBatch:
                                       self.cache.heads, _lib.stream_handle(self.cache.device)), 'dkv_pack_batch')
 
 
+def attend_projection(module, cache, qkv, position_embeddings):
+    """The packed-cache attention of one LlamaAttention from its joined projection qkv [1, n, (nq + 2 nkv) * d]:
+    split + RoPE + append (one launch when dkv_rope_pack covers it), then attend. Returns the attention output
+    [1, n, nq, d] (src/gpu_cache.py:164-174)."""
+    from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
+
+    from .gpu_ops import rope_qkv
+    hd, layer = module.head_dim, module.layer_idx
+    nq, nkv = module._qkv_sizes[0] // hd, module._qkv_sizes[1] // hd
+    packed = cache.append_projection(qkv, *position_embeddings, nq, layer) if nkv == cache.heads else None
+    if packed is not None:
+        q, k, v, past = packed
+    else:
+        roped = rope_qkv(qkv, *position_embeddings, nq, nkv, hd)  # split + RoPE in one launch
+        if roped is not None:
+            q, k, v = roped
+        else:
+            shape = qkv.shape[:-1]
+            q, k, v = qkv.split(module._qkv_sizes, dim=-1)
+            q = q.view(*shape, -1, hd).transpose(1, 2)
+            k = k.view(*shape, -1, hd).transpose(1, 2)
+            v = v.view(*shape, -1, hd).transpose(1, 2)
+            q, k = apply_rotary_pos_emb(q, k, *position_embeddings)
+        past = cache.append(k, v, layer)
+    return cache.attend(q, k, v, layer, past)
+
+
 def install_packed_attention(model):
     """Routes LlamaAttention through the packed cache when given a GPUCache (src/gpu_cache.py:151-183).
 
@@ -839,8 +866,6 @@ def install_packed_attention(model):
     transformers 4.x and the `past_key_values` keyword of 5.x.
     """
     from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
-
-    from .gpu_ops import rope_qkv
 
     def forward(module, hidden_states, position_embeddings=None, attention_mask=None, past_key_value=None,
                 cache_position=None, **kwargs):
@@ -855,32 +880,15 @@ def install_packed_attention(model):
         if kwargs.get('output_attentions', False):
             raise ValueError('Fused packed attention does not expose attention matrices')
         shape = hidden_states.shape[:-1]
-        roped = None
         if fused and hasattr(module, '_qkv_weight'):
             qkv = F.linear(hidden_states, module._qkv_weight)
-            hd = module.head_dim
-            nq, nkv = module._qkv_sizes[0] // hd, module._qkv_sizes[1] // hd
-            if nkv == cache.heads:
-                # split + RoPE + append in one launch (bit-equal to apply_rotary_pos_emb in bf16
-                # followed by append)
-                packed = cache.append_projection(qkv, *position_embeddings, nq, module.layer_idx)
-                if packed is not None:
-                    q, k, v, past = packed
-                    output = cache.attend(q, k, v, module.layer_idx, past)
-                    return module.o_proj(output.reshape(*shape, -1).contiguous()), None
-            # split + RoPE in one launch
-            roped = rope_qkv(qkv, *position_embeddings, nq, nkv, hd)
-            if roped is None:
-                q, k, v = qkv.split(module._qkv_sizes, dim=-1)
-        else:
-            q, k, v = module.q_proj(hidden_states), module.k_proj(hidden_states), module.v_proj(hidden_states)
-        if roped is not None:
-            q, k, v = roped
-        else:
-            q = q.view(*shape, -1, module.head_dim).transpose(1, 2)
-            k = k.view(*shape, -1, module.head_dim).transpose(1, 2)
-            v = v.view(*shape, -1, module.head_dim).transpose(1, 2)
-            q, k = apply_rotary_pos_emb(q, k, *position_embeddings)
+            output = attend_projection(module, cache, qkv, position_embeddings)
+            return module.o_proj(output.reshape(*shape, -1).contiguous()), None
+        q, k, v = module.q_proj(hidden_states), module.k_proj(hidden_states), module.v_proj(hidden_states)
+        q = q.view(*shape, -1, module.head_dim).transpose(1, 2)
+        k = k.view(*shape, -1, module.head_dim).transpose(1, 2)
+        v = v.view(*shape, -1, module.head_dim).transpose(1, 2)
+        q, k = apply_rotary_pos_emb(q, k, *position_embeddings)
         if fused:
             past = cache.append(k, v, module.layer_idx)
             output = cache.attend(q, k, v, module.layer_idx, past)

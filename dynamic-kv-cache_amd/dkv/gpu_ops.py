@@ -5,11 +5,17 @@ install_fused_ops. The reference keeps RMSNorm and SiLU*up as PyTorch library
 ops; here bf16 CUDA tensors go through one HIP launch each (libdkv's
 dkv_rms_norm and dkv_silu_mul), with the same bf16 rounding points as the
 torch compositions. rope_qkv() is the joined Q/K/V split plus RoPE of the
-patched attention forward in one launch (dkv_rope_qkv). The projections stay
-library GEMMs (one joined GEMM for Q/K/V and one for gate/up).
+patched attention forward in one launch (dkv_rope_qkv).
 
-Tensors the kernels do not cover (other dtypes, CPU tensors) take the
-reference's own torch composition.
+linear() is libdkv's short-chunk projection (dkv_linear): the joined GEMMs on
+MFMA with the RMSNorm before them and the residual add or SiLU*up after them
+folded in. install_fused_ops also patches LlamaDecoderLayer so that, on a
+packed GPUCache, a layer runs as five launches plus the attention: Q/K/V
+(with input_layernorm), split + RoPE + pack, attention, o_proj + residual,
+gate/up (with post_attention_layernorm) + SiLU*up, down_proj + residual.
+
+Tensors the kernels do not cover (other dtypes, CPU tensors, other shapes)
+take the reference's own torch composition.
 """
 import types
 
@@ -84,10 +90,84 @@ def rope_qkv(qkv, cos, sin, q_heads, kv_heads, head_dim=64):
     return q, k, v
 
 
-def install_fused_ops(text, state):
-    """Joins Q/K/V and gate/up weights and patches RMSNorm/MLP (src/gpu_ops.py:19-48).
+LINEAR_PLAIN, LINEAR_RESIDUAL, LINEAR_SILU_MUL = 0, 1, 2
 
-    `state['enabled']` switches between the joined path and the untouched upstream forwards.
+
+def _weight_rows(w):
+    return (w.dim() == 2 and w.is_cuda and w.dtype == torch.bfloat16 and w.stride(1) == 1
+            and w.stride(0) % 8 == 0 and w.data_ptr() % 16 == 0)
+
+
+def linear_covered(rows, weight, norm=False, epilogue=LINEAR_PLAIN):
+    """Whether dkv_linear has a launch for x [rows, weight.shape[1]] . weight^T with this prologue/epilogue."""
+    return _weight_rows(weight) and bool(_lib.load().dkv_linear_supported(
+        rows, weight.shape[0], weight.shape[1], int(norm), epilogue))
+
+
+def linear(x, weight, norm=None, eps=1e-6, residual=None, silu_mul=False):
+    """x [..., k] . weight[n, k]^T in one launch, optionally with RMSNorm(x) * norm first and the
+    residual add (out = residual + y) or SiLU*up over [gate | up] weight rows after; the rounding
+    points are the torch compositions'. Returns None when the kernel does not cover the inputs."""
+    epi = LINEAR_SILU_MUL if silu_mul else (LINEAR_RESIDUAL if residual is not None else LINEAR_PLAIN)
+    if not _fused(x) or not _weight_rows(weight) or x.shape[-1] != weight.shape[1]:
+        return None
+    x2 = _rows(x)
+    rows, k = x2.shape
+    n_out = weight.shape[0] // 2 if silu_mul else weight.shape[0]
+    if norm is not None and (not _fused(norm) or norm.dim() != 1 or norm.shape[0] != k or norm.stride(0) != 1
+                             or norm.data_ptr() % 16):
+        return None
+    r2 = None
+    if residual is not None:
+        if not _fused(residual) or residual.shape[-1] != n_out:
+            return None
+        r2 = residual.reshape(-1, n_out)
+        if r2.shape[0] != rows or r2.stride(-1) != 1 or r2.stride(0) % 4 or r2.data_ptr() % 8:
+            return None
+    if not _lib.load().dkv_linear_supported(rows, weight.shape[0], k, int(norm is not None), epi):
+        return None
+    out = torch.empty((rows, n_out), dtype=x.dtype, device=x.device)
+    _lib.check(_lib.load().dkv_linear(
+        x2.data_ptr(), x2.stride(0), weight.data_ptr(), weight.stride(0), rows, weight.shape[0], k,
+        None if norm is None else norm.data_ptr(), float(eps), epi, None if r2 is None else r2.data_ptr(),
+        0 if r2 is None else r2.stride(0), out.data_ptr(), out.stride(0), _lib.stream_handle(x.device)),
+        'dkv_linear')
+    return out.view(*x.shape[:-1], n_out)
+
+
+def fused_decoder_layer(layer, hidden_states, cache, position_embeddings):
+    """One LlamaDecoderLayer forward on a packed GPUCache as six launches plus the attention's
+    two; None when the layer, the inputs or the cache are outside what they cover."""
+    from .gpu_cache import GPUCache, attend_projection
+    attn, mlp = layer.self_attn, layer.mlp
+    ln1, ln2 = layer.input_layernorm, layer.post_attention_layernorm
+    h = hidden_states
+    if not (isinstance(cache, GPUCache) and cache.backend == 'fused' and position_embeddings is not None
+            and hasattr(attn, '_qkv_weight') and hasattr(mlp, '_gate_up_weight') and h.dim() == 3
+            and h.shape[0] == 1 and _fused(h) and attn.o_proj.bias is None and mlp.down_proj.bias is None
+            and getattr(ln1, 'weight', None) is not None and getattr(ln2, 'weight', None) is not None):
+        return None
+    n, width = h.shape[1], h.shape[2]
+    o_w, d_w = attn.o_proj.weight, mlp.down_proj.weight
+    if not (linear_covered(n, attn._qkv_weight, True, LINEAR_PLAIN)
+            and linear_covered(n, o_w, False, LINEAR_RESIDUAL) and o_w.shape[0] == width
+            and linear_covered(n, mlp._gate_up_weight, True, LINEAR_SILU_MUL)
+            and linear_covered(n, d_w, False, LINEAR_RESIDUAL) and d_w.shape[0] == width):
+        return None
+    x = h.reshape(n, width)
+    qkv = linear(x, attn._qkv_weight, norm=ln1.weight, eps=ln1.variance_epsilon)
+    o = attend_projection(attn, cache, qkv.view(1, n, -1), position_embeddings)
+    h2 = linear(o.view(n, -1), o_w, residual=x)
+    act = linear(h2, mlp._gate_up_weight, norm=ln2.weight, eps=ln2.variance_epsilon, silu_mul=True)
+    return linear(act, d_w, residual=h2).view(1, n, width)
+
+
+def install_fused_ops(text, state):
+    """Joins Q/K/V and gate/up weights and patches RMSNorm/MLP (src/gpu_ops.py:19-48), and the
+    decoder layers (fused_decoder_layer, transformers 5.x layer signature).
+
+    `state['enabled']` switches between the joined path and the untouched upstream forwards;
+    `state['layers']` (default True) enables the fused decoder layers on a packed cache.
     """
     def rms_forward(module, x):
         return cuda_rms(x, module.weight, module.variance_epsilon) if state['enabled'] else module._original_rms(x)
@@ -116,8 +196,21 @@ def install_fused_ops(text, state):
                 offset += n
         return joined
 
+    def layer_forward(module, hidden_states, *args, **kwargs):
+        if state['enabled'] and state.get('layers', True) and not args and not kwargs.get('output_attentions'):
+            cache = kwargs.get('past_key_values', kwargs.get('past_key_value'))
+            out = fused_decoder_layer(module, hidden_states, cache, kwargs.get('position_embeddings'))
+            if out is not None:
+                return out
+        return module._original_layer(hidden_states, *args, **kwargs)
+
+    import transformers
+    layers_return_tensors = int(transformers.__version__.split('.')[0]) >= 5
     for module in text.modules():
         name = module.__class__.__name__
+        if name == 'LlamaDecoderLayer' and layers_return_tensors and not hasattr(module, '_original_layer'):
+            module._original_layer = module.forward
+            module.forward = types.MethodType(layer_forward, module)
         if name == 'LlamaAttention' and all(m.bias is None for m in (module.q_proj, module.k_proj, module.v_proj)):
             module._qkv_weight = join([module.q_proj, module.k_proj, module.v_proj])
             module._qkv_sizes = [module.q_proj.out_features, module.k_proj.out_features, module.v_proj.out_features]

@@ -245,6 +245,30 @@ int dkv_rms_norm(const void* x, int64_t x_row_stride, const void* weight, void* 
 int dkv_silu_mul(const void* gate_up, int64_t row_stride, void* out, int64_t out_row_stride,
                  int32_t rows, int32_t inter, void* stream);
 
+/* Decoder projections of short chunks (1-100 rows) on MFMA:
+ *   out[rows, n_out] = epilogue(prologue(x) . w^T)
+ * x [rows, k] and w [n, k] bf16 with contiguous rows (k a multiple of 64),
+ * fp32 accumulation, bf16 out. These replace the library GEMMs and the
+ * PyTorch ops around them in the decoder layer that calls the packed cache
+ * (src/gpu_ops.py:19-48 joins the projections; src/gpu_cache.py:164-165, 183
+ * and transformers' LlamaDecoderLayer run them):
+ *   norm_weight != NULL: x rows pass through RMSNorm first, rounded as
+ *     bf16(bf16(x * rsqrt(mean(x^2) + eps)) * norm_weight) (src/gpu_ops.py:9-12);
+ *   DKV_LINEAR_PLAIN     out = bf16(acc), n_out = n;
+ *   DKV_LINEAR_RESIDUAL  out = bf16(residual + bf16(acc)), residual [rows, n];
+ *   DKV_LINEAR_SILU_MUL  w = [gate | up] (n = 2 n_out rows):
+ *     out[:, c] = bf16(bf16(silu(bf16(gate_c))) * bf16(up_c)) (src/gpu_ops.py:14-17).
+ * dkv_linear_supported says whether a shape has a launch (1) or not (0); an
+ * unsupported call returns DKV_EINVAL without touching the device. */
+#define DKV_LINEAR_PLAIN 0
+#define DKV_LINEAR_RESIDUAL 1
+#define DKV_LINEAR_SILU_MUL 2
+int dkv_linear_supported(int32_t rows, int32_t n, int32_t k, int32_t has_norm, int32_t epilogue);
+int dkv_linear(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride,
+               int32_t rows, int32_t n, int32_t k, const void* norm_weight, float eps,
+               int32_t epilogue, const void* residual, int64_t residual_row_stride,
+               void* out, int64_t out_row_stride, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

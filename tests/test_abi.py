@@ -251,3 +251,22 @@ def test_rope_pack_rejects_bad_arguments_without_touching_the_device():
     assert call(n=0, on_device=1) == _lib.DKV_EINVAL and 'device job' in lib.dkv_last_error().decode()
     assert lib.dkv_rope_pack(ok, 1600, ok, ok, 64, 64, 15, ok, ok, ok, None, 0, arena, 1 << 20, ok, 2, 5,
                              None) == _lib.DKV_EINVAL  # no job
+
+
+def test_linear_rejects_unsupported_shapes_without_touching_the_device():
+    lib = _lib.load()
+    ok = ctypes.c_void_p(4096)
+    assert lib.dkv_linear_supported(64, 1600, 960, 1, 0) == 1
+    assert lib.dkv_linear_supported(64, 5120, 960, 1, 2) == 1
+    assert lib.dkv_linear_supported(100, 960, 2560, 0, 1) == 1
+    assert lib.dkv_linear_supported(64, 960, 900, 0, 0) == 0  # k % 64
+    assert lib.dkv_linear_supported(64, 1000, 960, 0, 0) == 0  # n % 16
+    assert lib.dkv_linear_supported(64, 960, 2048, 1, 0) == 0  # norm needs k <= 1024
+    assert lib.dkv_linear_supported(64, 960, 960, 0, 3) == 0  # no such epilogue
+    assert lib.dkv_linear(ok, 960, ok, 960, 64, 960, 900, None, 1e-5, 0, None, 0, ok, 960, None) == _lib.DKV_EINVAL
+    assert 'dkv_linear' in lib.dkv_last_error().decode()
+    assert lib.dkv_linear(ok, 960, ok, 960, 64, 960, 960, None, 1e-5, 1, None, 0, ok, 960,
+                          None) == _lib.DKV_EINVAL  # residual epilogue without a residual
+    assert lib.dkv_linear(ctypes.c_void_p(4098), 960, ok, 960, 64, 960, 960, None, 1e-5, 0, None, 0, ok, 960,
+                          None) == _lib.DKV_EINVAL  # misaligned x
+    assert lib.dkv_linear(ok, 960, ok, 960, 0, 960, 960, None, 1e-5, 0, None, 0, ok, 960, None) == 0  # no rows
