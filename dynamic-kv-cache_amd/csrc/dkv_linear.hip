@@ -71,7 +71,8 @@ __global__ void __launch_bounds__(64 * WAVES) linear_kernel(const LinearArgs a) 
   const int rg = j % a.row_groups;
   const int ct = (j / a.row_groups) * 8 + xcd;
   if (ct >= a.n_tiles) return;  // uniform over the workgroup
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, col = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, col = lane & 15, g = lane >> 4;
   const int n0 = ct * 16 * NT;
 
   const uint16_t* wrow[NB];
@@ -80,132 +81,145 @@ __global__ void __launch_bounds__(64 * WAVES) linear_kernel(const LinearArgs a) 
     const int r = (EPI == EPI_SILU_MUL && nb >= NT) ? a.up + n0 + 16 * (nb - NT) + col : n0 + 16 * nb + col;
     wrow[nb] = a.w + (int64_t)r * a.ldw + 8 * g;
   }
+  // Rows past the end read the last row: x row j only reaches output row j,
+  // which is not stored.
   const uint16_t* xrow[RB];
-  bool xin[RB];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
-    const int row = (rg * RB + rb) * 16 + col;
-    xin[rb] = row < a.rows;
-    xrow[rb] = a.x + (int64_t)(xin[rb] ? row : 0) * a.ldx + 8 * g;
+    const int row = min((rg * RB + rb) * 16 + col, a.rows - 1);
+    xrow[rb] = a.x + (int64_t)row * a.ldx + 8 * g;
   }
 
+  // Every load of this wave's pairs (the host guarantees CH * WAVES >= kp) is
+  // issued before the first MFMA; p < kp is uniform over the wave.
+  Op8 xa[CH][2][RB], wa[CH][2][NB];
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int p = wave + WAVES * i;
+    if (p < a.kp) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int k = 64 * p + 32 * h;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) wa[i][h][nb].u = *reinterpret_cast<const u32x4*>(wrow[nb] + k);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) xa[i][h][rb].u = *reinterpret_cast<const u32x4*>(xrow[rb] + k);
+      }
+    }
+  }
+  if (NORM) {
+    __shared__ float ssum[WAVES][RB][16];
+    Op8 gn[CH][2];
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int p = wave + WAVES * i;
+      if (p < a.kp)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) gn[i][h].u = *reinterpret_cast<const u32x4*>(a.norm + 64 * p + 32 * h + 8 * g);
+    }
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < CH; ++i) {
+        if (wave + WAVES * i < a.kp)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float lo = bf16_lo(xa[i][h][rb].u[e]), hi = bf16_hi(xa[i][h][rb].u[e]);
+              ss = __fmaf_rn(lo, lo, ss);
+              ss = __fmaf_rn(hi, hi, ss);
+            }
+      }
+      ss = lane_group_sum(ss);
+      if (g == 0) ssum[wave][rb][col] = ss;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      float tot = 0.f;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) tot += ssum[w][rb][col];
+      const float rstd = 1.f / sqrtf(tot / (float)a.k + a.eps);
+#pragma unroll
+      for (int i = 0; i < CH; ++i) {
+        if (wave + WAVES * i < a.kp)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const uint32_t xv = xa[i][h][rb].u[e], gv = gn[i][h].u[e];
+              xa[i][h][rb].u[e] = pack_bf16(round_bf16(bf16_lo(xv) * rstd) * bf16_lo(gv),
+                                            round_bf16(bf16_hi(xv) * rstd) * bf16_hi(gv));
+            }
+      }
+    }
+  }
   f32x4_t acc[RB][NB];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[rb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  __shared__ float ssum[NORM ? WAVES : 1][RB][16];
-  const int per_wave = (a.kp + WAVES - 1) / WAVES;  // pairs of this wave (upper bound)
-  for (int c0 = 0; c0 < per_wave; c0 += CH) {
-    Op8 xa[CH][2][RB], wa[CH][2][NB];
 #pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const int p = wave + WAVES * (c0 + i);
-      if (p < a.kp) {
+  for (int i = 0; i < CH; ++i) {
+    if (wave + WAVES * i < a.kp)
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int k = 64 * p + 32 * h;
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
-          for (int nb = 0; nb < NB; ++nb) wa[i][h][nb].u = *reinterpret_cast<const u32x4*>(wrow[nb] + k);
+        for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-          for (int rb = 0; rb < RB; ++rb)
-            xa[i][h][rb].u = xin[rb] ? *reinterpret_cast<const u32x4*>(xrow[rb] + k) : u32x4{0, 0, 0, 0};
-        }
-      }
-    }
-    if (NORM) {  // the host guarantees one chunk (CH * WAVES >= kp): every wave holds all of its pairs
-      Op8 gn[CH][2];
-#pragma unroll
-      for (int i = 0; i < CH; ++i) {
-        const int p = wave + WAVES * (c0 + i);
-        if (p < a.kp)
-#pragma unroll
-          for (int h = 0; h < 2; ++h)
-            gn[i][h].u = *reinterpret_cast<const u32x4*>(a.norm + 64 * p + 32 * h + 8 * g);
-      }
-      float ss[RB];
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        ss[rb] = 0.f;
-#pragma unroll
-        for (int i = 0; i < CH; ++i) {
-          if (wave + WAVES * (c0 + i) < a.kp)
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                const float lo = bf16_lo(xa[i][h][rb].u[e]), hi = bf16_hi(xa[i][h][rb].u[e]);
-                ss[rb] = __fmaf_rn(lo, lo, ss[rb]);
-                ss[rb] = __fmaf_rn(hi, hi, ss[rb]);
-              }
-        }
-        ss[rb] = lane_group_sum(ss[rb]);
-        if (g == 0) ssum[wave][rb][col] = ss[rb];
-      }
-      __syncthreads();
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        float tot = 0.f;
-#pragma unroll
-        for (int w = 0; w < WAVES; ++w) tot += ssum[w][rb][col];
-        const float rstd = 1.f / sqrtf(tot / (float)a.k + a.eps);
-#pragma unroll
-        for (int i = 0; i < CH; ++i) {
-          if (wave + WAVES * (c0 + i) < a.kp)
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                const uint32_t xv = xa[i][h][rb].u[e], gv = gn[i][h].u[e];
-                xa[i][h][rb].u[e] = pack_bf16(round_bf16(bf16_lo(xv) * rstd) * bf16_lo(gv),
-                                              round_bf16(bf16_hi(xv) * rstd) * bf16_hi(gv));
-              }
-        }
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      if (wave + WAVES * (c0 + i) < a.kp)
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb)
-              acc[rb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[i][h][nb].v, xa[i][h][rb].v, acc[rb][nb], 0, 0, 0);
-    }
+          for (int nb = 0; nb < NB; ++nb)
+            acc[rb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[i][h][nb].v, xa[i][h][rb].v, acc[rb][nb], 0, 0, 0);
   }
 
-  // Every wave stores its partials; one wave per output tile adds them up in
-  // wave order.
-  __shared__ f32x4_t red[WAVES][RB * NB][64];
+  // The waves' partials are summed in wave order through LDS, TP tiles per
+  // phase (at most 32 KB of partials). Output tile o = (rb, nt) belongs to
+  // wave o % WAVES, which sums its gate (and up) partial tiles and runs the
+  // epilogue.
+  constexpr int TILES = RB * NB, OUT = RB * NT;
+  constexpr int TP = TILES < 32 / WAVES ? TILES : 32 / WAVES;
+  __shared__ f32x4_t red[WAVES][TP][64];
+  f32x4_t gsum[OUT], usum[OUT];
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb)
+  for (int ph = 0; ph < (TILES + TP - 1) / TP; ++ph) {
+    if (ph) __syncthreads();  // the previous phase's partials have been read
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) red[wave][rb * NB + nb][lane] = acc[rb][nb];
-  __syncthreads();
-  auto tile_sum = [&](int rb, int nb) {
-    f32x4_t s = red[0][rb * NB + nb][lane];
-#pragma unroll
-    for (int w = 1; w < WAVES; ++w) {
-      const f32x4_t v = red[w][rb * NB + nb][lane];
-      s[0] += v[0];
-      s[1] += v[1];
-      s[2] += v[2];
-      s[3] += v[3];
+    for (int j = 0; j < TP; ++j) {
+      const int t = ph * TP + j;
+      if (t < TILES) red[wave][j][lane] = acc[t / NB][t % NB];
     }
-    return s;
-  };
-  for (int t = wave; t < RB * NT; t += WAVES) {
-    const int rb = t / NT, nt = t - rb * NT;
-    const f32x4_t s = tile_sum(rb, nt);
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < TP; ++j) {
+      const int t = ph * TP + j;
+      if (t >= TILES) continue;
+      const int rb = t / NB, nb = t % NB;
+      const int o = rb * NT + nb % NT;  // output tile of this partial tile
+      if (o % WAVES != wave) continue;
+      f32x4_t s = red[0][j][lane];
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) {
+        const f32x4_t v = red[w][j][lane];
+        s[0] += v[0];
+        s[1] += v[1];
+        s[2] += v[2];
+        s[3] += v[3];
+      }
+      if (nb < NT) gsum[o] = s;
+      else usum[o] = s;
+    }
+  }
+#pragma unroll
+  for (int o = 0; o < OUT; ++o) {
+    if (o % WAVES != wave) continue;
+    const int rb = o / NT, nt = o % NT;
     const int row = (rg * RB + rb) * 16 + col;
     if (row >= a.rows) continue;
     const int c = n0 + 16 * nt + 4 * g;
     float y[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) y[e] = round_bf16(s[e]);
+    for (int e = 0; e < 4; ++e) y[e] = round_bf16(gsum[o][e]);
     if (EPI == EPI_RESIDUAL) {
       const uint2 r = *reinterpret_cast<const uint2*>(a.res + (int64_t)row * a.ldr + c);
       y[0] += bf16_lo(r.x);
@@ -213,11 +227,11 @@ __global__ void __launch_bounds__(64 * WAVES) linear_kernel(const LinearArgs a) 
       y[2] += bf16_lo(r.y);
       y[3] += bf16_hi(r.y);
     } else if (EPI == EPI_SILU_MUL) {
-      const f32x4_t u = tile_sum(rb, NT + nt);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) y[e] = round_bf16(y[e] / (1.f + expf(-y[e]))) * round_bf16(u[e]);
+      for (int e = 0; e < 4; ++e) y[e] = round_bf16(y[e] / (1.f + expf(-y[e]))) * round_bf16(usum[o][e]);
     }
-    *reinterpret_cast<uint2*>(a.out + (int64_t)row * a.ldo + c) = make_uint2(pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3]));
+    *reinterpret_cast<uint2*>(a.out + (int64_t)row * a.ldo + c) =
+        make_uint2(pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3]));
   }
 }
 
@@ -225,27 +239,29 @@ bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 // Launch shapes, from graph-replay timings of the 960-wide decoder's projections at 64 rows
 // (weights streamed from HBM): narrow outputs use one 16-row block per workgroup (more
-// workgroups), the joined gate/up projection 32 rows (each weight tile read twice per 64 rows).
+// workgroups); the joined gate/up projection 32 x rows and 32 output columns per workgroup
+// (160 workgroups at 64 rows, all resident at once). With the RMSNorm prologue every
+// workgroup normalizes its own x rows, so fewer rows per workgroup cost less VALU time than
+// the second read of each weight tile they bring (64 rows per workgroup: 13.3 us, 32: 11.4 us).
 struct Shape {
   int ch, nt, waves, rb;
 };
 
-constexpr int MAX_CH = 5;       // pairs per wave and chunk
-constexpr int MAX_NORM_CH = 2;  // with the RMSNorm prologue a row's pairs must fit one chunk
-                                // (k <= 1024), which also keeps those variants out of scratch
+constexpr int MAX_CH = 5;       // pairs per wave: k <= 5 * 8 * 64 = 2560
+constexpr int MAX_NORM_CH = 2;  // with the RMSNorm prologue (k <= 1024), which keeps those
+                                // variants out of scratch
 
 Shape pick(int n_out, int kp, int epilogue) {
   Shape s;
   s.waves = 8;
-  if (epilogue == EPI_SILU_MUL) {  // gate and up blocks: two weight tiles per workgroup
-    s.nt = 1;
+  if (epilogue == EPI_SILU_MUL) {  // 32 gate and 32 up weight rows, 32 x rows
+    s.nt = 2;
     s.rb = 2;
   } else {
     s.nt = (n_out % 32 == 0 && n_out / 16 > 64) ? 2 : 1;
     s.rb = 1;
   }
-  const int per = (kp + s.waves - 1) / s.waves;
-  s.ch = per <= MAX_CH ? per : 4;
+  s.ch = (kp + s.waves - 1) / s.waves;  // every pair of a wave in registers at once
   return s;
 }
 
@@ -267,7 +283,9 @@ void launch_ch(int ch, const LinearArgs& a, hipStream_t st) {
       case 2: launch_one<2, NT, WAVES, RB, EPI, NORM>(a, st); break;
       case 3: launch_one<3, NT, WAVES, RB, EPI, NORM>(a, st); break;
       case 4: launch_one<4, NT, WAVES, RB, EPI, NORM>(a, st); break;
-      default: launch_one<MAX_CH, NT, WAVES, RB, EPI, NORM>(a, st); break;
+      default:
+        if constexpr (EPI != EPI_SILU_MUL) launch_one<MAX_CH, NT, WAVES, RB, EPI, NORM>(a, st);
+        break;  // dkv_linear_supported rules out the rest
     }
   }
 }
@@ -275,7 +293,7 @@ void launch_ch(int ch, const LinearArgs& a, hipStream_t st) {
 template <int EPI, bool NORM>
 void launch_epi(const Shape& s, const LinearArgs& a, hipStream_t st) {
   if constexpr (EPI == EPI_SILU_MUL) {
-    launch_ch<1, 8, 2, EPI, NORM>(s.ch, a, st);
+    launch_ch<2, 8, 2, EPI, NORM>(s.ch, a, st);
   } else {
     if (s.nt == 2) launch_ch<2, 8, 1, EPI, NORM>(s.ch, a, st);
     else launch_ch<1, 8, 1, EPI, NORM>(s.ch, a, st);
@@ -295,7 +313,8 @@ int dkv_linear_supported(int32_t rows, int32_t n, int32_t k, int32_t has_norm, i
   if (epilogue == EPI_SILU_MUL && (n & 1)) return 0;
   if (n_out % 16) return 0;
   const Shape s = pick(n_out, k / 64, epilogue);
-  if (has_norm && (s.ch > MAX_NORM_CH || s.ch * s.waves < k / 64)) return 0;  // a row's pairs in one chunk
+  const int max_ch = has_norm ? MAX_NORM_CH : (epilogue == EPI_SILU_MUL ? 4 : MAX_CH);  // register budget
+  if (s.ch > max_ch) return 0;
   if (s.nt == 2 && n_out % 32) return 0;
   return 1;
 }
