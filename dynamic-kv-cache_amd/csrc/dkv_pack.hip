@@ -287,16 +287,63 @@ __device__ __forceinline__ u32x4 rope8(const u32x4& x, const u32x4& partner, con
   return y;
 }
 
+// Packs one row held by 8 lanes (lane c of the row holds columns [8c, 8c + 8)
+// in w): min/max over the row through the 8 lanes, then the arithmetic of
+// pack_loaded (every lane of the row forms the same a, s and 1/s) and quantize8
+// on the lane's 8 elements. Lanes of rows r >= nrows still take part in the
+// exchanges but store nothing.
+template <int BITS>
+__device__ __forceinline__ void pack_row8(const dkv_pack_job& j, int kv, int head, int tok, bool valid, int c,
+                                          const u32x4& w, uint8_t* arena, int layers, int heads) {
+  float x[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    x[2 * e] = bf16_lo(w[e]);
+    x[2 * e + 1] = bf16_hi(w[e]);
+  }
+  if (BITS == 16) {
+    if (valid) *reinterpret_cast<u32x4*>(row_dst(j, kv, head, tok, arena, layers, heads).payload + 16 * c) = w;
+    return;
+  }
+  float lo = x[0], hi = x[0];
+#pragma unroll
+  for (int e = 1; e < 8; ++e) {
+    lo = fminf(lo, x[e]);
+    hi = fmaxf(hi, x[e]);
+  }
+#pragma unroll
+  for (int o = 1; o < 8; o <<= 1) {
+    lo = fminf(lo, __shfl_xor(lo, o));
+    hi = fmaxf(hi, __shfl_xor(hi, o));
+  }
+  const float a = lo;
+  const float span = hi - a;
+  const float s = span > 0.0f ? __fdiv_rn(span, BITS == 4 ? 15.0f : 255.0f) : 1.0f;
+  const float rs = __builtin_amdgcn_rcpf(s);
+  const bool fast = s >= 0x1p-126f && s <= 0x1p125f;
+  uint32_t out[2];
+  quantize8<BITS>(x, a, s, rs, fast, out);
+  if (!valid) return;
+  const RowDst d = row_dst(j, kv, head, tok, arena, layers, heads);
+  if (BITS == 4) *reinterpret_cast<uint32_t*>(d.payload + 4 * c) = out[0];
+  else *reinterpret_cast<uint2*>(d.payload + 8 * c) = make_uint2(out[0], out[1]);
+  if (c == 0) *d.meta = make_float2(a, s);
+}
+
 // Joined Q/K/V projection rows -> RoPE -> q, k, v ([heads, n, 64] each) with K
 // and V also packed into the job's segment: the projection split,
 // apply_rotary_pos_emb and GPUCache.append of the patched attention forward
 // (src/gpu_cache.py:164-172) in one launch. One wave per (projection head,
-// 64-token slice): heads [0, q_heads) are Q, then `heads` K heads (rotated,
-// packed), then `heads` V heads (packed). The packed bytes come from the same
-// pack_loaded as dkv_pack on the same bf16 rows, so they are identical to a
-// RoPE launch followed by dkv_pack. With DEVJOB the job is read from device
-// memory when the kernel runs (HIP graph replays); the projection, not the
-// job's k/v pointers, is the source.
+// 8-token slice), 8 lanes per token row (16 bytes each): heads [0, q_heads)
+// are Q, then `heads` K heads (rotated, packed), then `heads` V heads
+// (packed). A 64-token chunk is 25 x 8 waves at the 960-wide decoder's
+// shapes, so the per-row work (one row's quantization spread over its 8
+// lanes) runs on many CUs at once; the arithmetic is quantize8's, so the bytes
+// equal dkv_pack's for the same bf16 rows. With DEVJOB the job is read from
+// device memory when the kernel runs (HIP graph replays); the projection, not
+// the job's k/v pointers, is the source.
+constexpr int RP_ROWS = 8;  // token rows per wave
+
 template <bool DEVJOB>
 __global__ void __launch_bounds__(PACK_THREADS)
 rope_pack_kernel(const uint16_t* __restrict__ qkv, int64_t qkv_stride, const uint16_t* __restrict__ cosv,
@@ -304,66 +351,43 @@ rope_pack_kernel(const uint16_t* __restrict__ qkv, int64_t qkv_stride, const uin
                  uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_out, uint16_t* __restrict__ v_out,
                  dkv_pack_job hjob, const dkv_pack_job* __restrict__ djob, uint8_t* arena, dkv_tile* tiles,
                  int layers, int heads) {
-  __shared__ __attribute__((aligned(16))) uint8_t stage[PACK_THREADS / 64][WAVE_LDS];
-  uint8_t* lds = stage[threadIdx.x >> 6];
   const int gw = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * (PACK_THREADS / 64) + (threadIdx.x >> 6)));
-  const int slices = (n + WAVE_ROWS - 1) / WAVE_ROWS;
+  const int slices = (n + RP_ROWS - 1) / RP_ROWS;
   const int hh = gw / slices;
   if (hh >= q_heads + 2 * heads) return;
-  const int tok0 = (gw - hh * slices) * WAVE_ROWS;
-  const int nrows = min(WAVE_ROWS, n - tok0);
   const int lane = threadIdx.x & 63;
   const int c = lane & 7;
+  const int tok = (gw - hh * slices) * RP_ROWS + (lane >> 3);
+  const bool valid = tok < n;
+  const int t = valid ? tok : n - 1;  // rows past the end read the last row and store nothing
   const bool is_v = hh >= q_heads + heads;
 
-  u32x4 w[8], cs[8], sn[8];
-  const uint16_t* src = qkv + hh * D + 8 * c;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int r = 8 * i + (lane >> 3);
-    w[i] = r < nrows ? *reinterpret_cast<const u32x4*>(src + (tok0 + r) * qkv_stride) : u32x4{0, 0, 0, 0};
-  }
+  u32x4 w = *reinterpret_cast<const u32x4*>(qkv + (int64_t)t * qkv_stride + hh * D + 8 * c);
   if (!is_v) {
+    const int64_t o = (int64_t)t * cs_stride + 8 * c;
+    const u32x4 cs = *reinterpret_cast<const u32x4*>(cosv + o);
+    const u32x4 sn = *reinterpret_cast<const u32x4*>(sinv + o);
+    // rotate_half pairs column d with d +- 32: lane c with lane c ^ 4 of the same row
+    u32x4 p;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = 8 * i + (lane >> 3);
-      const int64_t o = (int64_t)(tok0 + r) * cs_stride + 8 * c;
-      cs[i] = r < nrows ? *reinterpret_cast<const u32x4*>(cosv + o) : u32x4{0, 0, 0, 0};
-      sn[i] = r < nrows ? *reinterpret_cast<const u32x4*>(sinv + o) : u32x4{0, 0, 0, 0};
-    }
-    // rotate_half pairs column d with d +- 32, i.e. lane c with lane c ^ 4 of
-    // the same row: exchange through the wave's LDS region.
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      *reinterpret_cast<u32x4*>(lds + (8 * i + (lane >> 3)) * LROW + 16 * c) = w[i];
-    wave_sync_lds();
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const u32x4 p = *reinterpret_cast<const u32x4*>(lds + (8 * i + (lane >> 3)) * LROW + 16 * (c ^ 4));
-      w[i] = rope8(w[i], p, cs[i], sn[i], c < 4);
-    }
-    wave_sync_lds();  // every lane has read its partner before the region is reused
+    for (int e = 0; e < 4; ++e) p[e] = __shfl_xor(w[e], 4);
+    w = rope8(w, p, cs, sn, c < 4);
   }
   uint16_t* dst = hh < q_heads ? q_out + (int64_t)hh * n * D
                                : (is_v ? v_out + (int64_t)(hh - q_heads - heads) * n * D
                                        : k_out + (int64_t)(hh - q_heads) * n * D);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int r = 8 * i + (lane >> 3);
-    if (r < nrows) *reinterpret_cast<u32x4*>(dst + (int64_t)(tok0 + r) * D + 8 * c) = w[i];
-  }
+  if (valid) *reinterpret_cast<u32x4*>(dst + (int64_t)tok * D + 8 * c) = w;
 
   const dkv_pack_job j = DEVJOB ? *djob : hjob;
   if (gw == 0 && j.write_tiles) write_segment_tiles(j, layers, heads, tiles);
   if (hh < q_heads) return;
-  const int np = min(WAVE_ROWS, min(j.n, n) - tok0);  // rows of this slice the job packs
-  if (np <= 0) return;
+  const bool packs = valid && tok < j.n;  // rows the job packs
   const int kv = is_v ? 1 : 0;
   const int head = hh - q_heads - kv * heads;
   const int bits = __builtin_amdgcn_readfirstlane(j.bits);
-  if (bits == 4) pack_loaded<4>(j, kv, head, tok0, np, w, arena, layers, heads, lds);
-  else if (bits == 8) pack_loaded<8>(j, kv, head, tok0, np, w, arena, layers, heads, lds);
-  else pack_loaded<16>(j, kv, head, tok0, np, w, arena, layers, heads, lds);
+  if (bits == 4) pack_row8<4>(j, kv, head, tok, packs, c, w, arena, layers, heads);
+  else if (bits == 8) pack_row8<8>(j, kv, head, tok, packs, c, w, arena, layers, heads);
+  else pack_row8<16>(j, kv, head, tok, packs, c, w, arena, layers, heads);
 }
 
 static int pack_waves(int n, int heads) { return 2 * heads * ((n + WAVE_ROWS - 1) / WAVE_ROWS); }
@@ -550,7 +574,7 @@ int dkv_rope_pack(const void* qkv, int64_t qkv_row_stride, const void* cos, cons
                        static_cast<uint8_t*>(arena), tiles, layers, heads);
     return (int)hipGetLastError();
   }
-  const int64_t waves = (int64_t)(q_heads + 2 * heads) * ((n + WAVE_ROWS - 1) / WAVE_ROWS);
+  const int64_t waves = (int64_t)(q_heads + 2 * heads) * ((n + RP_ROWS - 1) / RP_ROWS);
   const unsigned blocks = (unsigned)((waves + PACK_THREADS / 64 - 1) / (PACK_THREADS / 64));
   const dkv_pack_job none = {};
   const auto* qp = static_cast<const uint16_t*>(qkv);
