@@ -100,7 +100,10 @@ class StreamingDecoder:
         graphed = self.graphs and cache is self._cache
         for i, (emb, b) in enumerate(zip(frames, bits)):
             cache.select(b, i)
-            if graphed and i > 0 and emb.shape[1] == frames[0].shape[1]:
+            # The first frame of the first request runs eagerly (it warms up the library paths
+            # the capture records); every other frame of the captured length replays the graph.
+            captured = self._frame is not None and self._frame['chunk'] == emb.shape[1]
+            if graphed and (i > 0 or captured) and emb.shape[1] == frames[0].shape[1]:
                 self._graph_frame(cache, emb)
             else:
                 self.forward(cache, embeddings=emb)
