@@ -414,7 +414,10 @@ class GPUCache(_CacheBase):
         lib = _lib.load()
         need = lib.dkv_attend_workspace_bytes(ctypes.byref(a))
         if need:
-            ws = self._workspace_for(need)
+            # A captured graph keeps the workspace it recorded: graph launches use their
+            # GraphSteps' own buffer, so an ordinary call that grows the cache's buffer can never
+            # free memory a graph still writes.
+            ws = self._graph.workspace(need) if self._graph is not None else self._workspace_for(need)
             a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
         _lib.check(lib.dkv_attend(ctypes.byref(a), _lib.stream_handle(self.device)), 'dkv_attend')
         return out
@@ -484,8 +487,9 @@ class GPUCache(_CacheBase):
         graph and replayed as the history grows. Before capturing, and before every replay, call
         graph_step(); in this mode append() and attend() only launch (no bookkeeping).
 
-        `q_heads` pre-sizes the attention workspace for the launch bounds (so nothing is allocated
-        while capturing). `steps` re-attaches the GraphSteps of an earlier capture on this cache.
+        `q_heads` pre-sizes the steps' attention workspace for the launch bounds (so nothing is
+        allocated while capturing); graph launches use that buffer, never the one ordinary calls
+        grow. `steps` re-attaches the GraphSteps of an earlier capture on this cache.
         """
         if len(set(self.seen)) != 1:
             raise ValueError('graph steps need every layer at the same length')
@@ -493,7 +497,7 @@ class GPUCache(_CacheBase):
             raise ValueError('these graph steps belong to another cache')
         self._graph = steps or GraphSteps(self, chunk)
         if q_heads:
-            self._workspace_for(self._graph.workspace_bytes(q_heads))
+            self._graph.workspace(self._graph.workspace_bytes(q_heads))
         return self._graph
 
     def end_graph_steps(self):
@@ -639,6 +643,13 @@ class GraphSteps:
         # Launch bounds: the largest history a chunk can attend to in this cache.
         self.past_bound = cache.capacity - chunk
         self.tiles_bound = cache.tiles.shape[0]
+        self.ws = None  # attention workspace of the recorded launches (grow-only, before capture)
+
+    def workspace(self, nbytes):
+        if self.ws is None or self.ws.numel() < nbytes:
+            with torch.inference_mode(False):
+                self.ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=self.cache.device)
+        return self.ws
 
     def step(self):
         c, n = self.cache, self.chunk

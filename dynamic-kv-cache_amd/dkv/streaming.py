@@ -55,7 +55,7 @@ class StreamingDecoder:
         install_fused_ops(self.text, self.ops_state)
         install_packed_attention(model)
         self._cache = None  # reused across requests when graphs=True (a captured graph records its buffers)
-        self._frame = None  # the captured frame forward
+        self._graphs = {}  # chunk length -> captured forward of that length on self._cache
 
     @property
     def device(self):
@@ -96,15 +96,18 @@ class StreamingDecoder:
         if cache is None:
             cache = self._reused_cache(total) if self.graphs else self.create_cache(total)
         cache.select(16, -1)
-        self.forward(cache, ids=prefix_ids)
         graphed = self.graphs and cache is self._cache
+        # The first request's prefix and first frame run eagerly (they warm up the library paths
+        # a capture records); after that every chunk replays the captured forward of its length
+        # (captured on first use).
+        if graphed and self._graphs:
+            self._graph_chunk(cache, self.text.get_input_embeddings()(prefix_ids.to(self.device)))
+        else:
+            self.forward(cache, ids=prefix_ids)
         for i, (emb, b) in enumerate(zip(frames, bits)):
             cache.select(b, i)
-            # The first frame of the first request runs eagerly (it warms up the library paths
-            # the capture records); every other frame of the captured length replays the graph.
-            captured = self._frame is not None and self._frame['chunk'] == emb.shape[1]
-            if graphed and (i > 0 or captured) and emb.shape[1] == frames[0].shape[1]:
-                self._graph_frame(cache, emb)
+            if graphed and (i > 0 or self._graphs):
+                self._graph_chunk(cache, emb)
             else:
                 self.forward(cache, embeddings=emb)
         cache.select(16, -1)
@@ -115,16 +118,16 @@ class StreamingDecoder:
     def _reused_cache(self, total):
         if self._cache is None or self._cache.capacity < total:
             self._cache = self.create_cache(max(total, 8192))
-            self._frame = None  # a captured graph records the old cache's buffers
+            self._graphs = {}  # a captured graph records the old cache's buffers
         else:
             self._cache.reset()
         return self._cache
 
-    def _graph_frame(self, cache, emb):
-        """One frame as a replay of the captured forward (captured on first use)."""
-        fg = self._frame
-        if fg is None or fg['chunk'] != emb.shape[1]:
-            self._capture_frame(cache, emb)
+    def _graph_chunk(self, cache, emb):
+        """One chunk as a replay of the captured forward of its length (captured on first use)."""
+        fg = self._graphs.get(emb.shape[1])
+        if fg is None:
+            self._capture_chunk(cache, emb)
             return
         cache.begin_graph_steps(fg['chunk'], steps=fg['steps'])
         try:
@@ -135,7 +138,7 @@ class StreamingDecoder:
         finally:
             cache.end_graph_steps()
 
-    def _capture_frame(self, cache, emb):
+    def _capture_chunk(self, cache, emb):
         chunk = emb.shape[1]
         static_emb = emb.clone()
         arange = torch.arange(chunk, device=self.device)
@@ -153,7 +156,7 @@ class StreamingDecoder:
             graph.replay()
         finally:
             cache.end_graph_steps()
-        self._frame = dict(chunk=chunk, graph=graph, steps=steps, emb=static_emb, pos=pos, arange=arange)
+        self._graphs[chunk] = dict(chunk=chunk, graph=graph, steps=steps, emb=static_emb, pos=pos, arange=arange)
 
     @staticmethod
     def _mean_loglik(logits, targets):

@@ -114,3 +114,41 @@ def test_graph_steps_created_in_inference_mode_step_outside_it(cuda):
     c.end_graph_steps()
     torch.cuda.synchronize()
     assert c.seen == [192, 192] and [s.bits for s in c.segments] == [4, 8, 16]
+
+
+def test_graph_launches_keep_their_workspace(cuda):
+    """A captured attention launch keeps the workspace it recorded: an ordinary call on the same
+    cache that needs a larger workspace afterwards (a 300-token chunk) must not move it, so the
+    next replay still equals an ordinary call of the same step, bit for bit."""
+    announce('cache: graph workspace survives a larger ordinary call')
+    g = torch.Generator().manual_seed(41)
+    hist = [torch.randn(1, 5, 128, 64, generator=g).to(torch.bfloat16).to(cuda) for _ in range(2)]
+    q = torch.randn(1, 15, 64, 64, generator=g).to(torch.bfloat16).to(cuda)
+    k = torch.randn(1, 5, 64, 64, generator=g).to(torch.bfloat16).to(cuda)
+    v = torch.randn(1, 5, 64, 64, generator=g).to(torch.bfloat16).to(cuda)
+
+    def filled():
+        c = GPUCache(None, layers=1, heads=5, max_tokens=1024)
+        c.select(4, 0)
+        c.append(*hist, 0)
+        c.select(8, 1)
+        return c
+
+    ref_cache = filled()
+    ref = ref_cache.attend(q, k, v, 0, ref_cache.append(k, v, 0))
+    c = filled()
+    steps = c.begin_graph_steps(64, q_heads=15)
+    past = c.graph_step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        c.append(k, v, 0)
+        out = c.attend(q, k, v, 0, past)
+    steps.upload()
+    c.end_graph_steps()
+    qb = torch.randn(1, 15, 300, 64, generator=g).to(torch.bfloat16).to(cuda)
+    kb = torch.randn(1, 5, 300, 64, generator=g).to(torch.bfloat16).to(cuda)
+    c.attend(qb, kb, kb, 0, 128)  # grows the cache's own workspace
+    graph.replay()
+    torch.cuda.synchronize()
+    assert past == 128 and torch.equal(out, ref)

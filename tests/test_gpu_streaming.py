@@ -117,7 +117,7 @@ def test_graph_replayed_ingest_matches_eager(cuda):
     eager_cache, eager = run()
     dec.graphs = True
     graph_cache, first = run()
-    assert dec._frame is not None and graph_cache is dec._cache
+    assert 64 in dec._graphs and graph_cache is dec._cache
     assert graph_cache.plan == eager_cache.plan and graph_cache.seen == eager_cache.seen
     assert [s.frame for s in graph_cache.segments] == [s.frame for s in eager_cache.segments]
     assert graph_cache.accounting()['precision_token_counts'] == eager_cache.accounting()['precision_token_counts']
@@ -125,7 +125,8 @@ def test_graph_replayed_ingest_matches_eager(cuda):
         for a, b in zip(graph_cache.materialize(layer), eager_cache.materialize(layer)):
             assert torch.equal(a, b)
     assert torch.equal(first, eager), (first - eager).abs().max().item()
-    _, second = run()
+    _, second = run()  # the prefix now replays a captured 16-token forward as well
+    assert 16 in dec._graphs
     assert torch.equal(first, second)
     dec.graphs = False
 
