@@ -8,9 +8,12 @@
 // Work split: a workgroup owns one KV head, one group of query rows (all GQA
 // heads of that KV head share each K/V tile) and one contiguous range of
 // "units" (history tiles, then 64-token pieces of the current chunk). With more
-// than one range per head, each workgroup writes unnormalized partial
-// (O, max, sum) and combine_kernel merges them with the usual log-sum-exp
-// rescaling. Softmax runs in base 2: x = score * scale * log2(e).
+// than one range per head, each workgroup writes partial (O, max, sum) and a
+// second kernel merges them with the usual log-sum-exp rescaling:
+// combine_kernel for precision 1 (unnormalized O in fp32), combine_half_kernel
+// for precision 0, the bf16 path (O / sum in fp16: 2^-11 of the normalized
+// value, well under the bf16 output's rounding, at half the partial traffic).
+// Softmax runs in base 2: x = score * scale * log2(e).
 #include "dkv_attn_common.h"
 
 namespace dkv {
@@ -203,7 +206,11 @@ attn_vec_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ part
       else static_cast<uint16_t*>(a.out)[off] = (uint16_t)f32_to_bf16_rne(o);
     } else {
       const int64_t base = ((int64_t)h * splits + split) * R + r;
-      __builtin_nontemporal_store(acc[i], part_o + base * D + lane);  // no dirty L2 lines at kernel end
+      if (PREC)
+        __builtin_nontemporal_store(acc[i], part_o + base * D + lane);  // no dirty L2 lines at kernel end
+      else  // O / l in fp16, half_slot() order
+        __builtin_nontemporal_store((_Float16)(sm[i] > 0.f ? acc[i] / sm[i] : 0.f),
+                                    reinterpret_cast<_Float16*>(part_o) + base * D + half_slot(lane));
       if (lane == 0) {
         __builtin_nontemporal_store(mx[i], reinterpret_cast<float*>(part_ml + base));
         __builtin_nontemporal_store(sm[i], reinterpret_cast<float*>(part_ml + base) + 1);
@@ -261,6 +268,88 @@ combine_kernel(dkv_attn_args a, int splits, const float* __restrict__ part_o,
   const int64_t off = (int64_t)m * a.out_tok_stride + (int64_t)(h * G + g) * a.out_head_stride + lane;
   if (a.out_dtype == 1) static_cast<float*>(a.out)[off] = out;
   else static_cast<uint16_t*>(a.out)[off] = (uint16_t)f32_to_bf16_rne(out);
+}
+
+// Precision-0 merge (fp16 O / sum partials, 128 bytes per row in half_slot()
+// order): one wave per query row. Lane l = 8 j + c reads 16-byte chunk c of
+// split s0 + 8 i + j for i = 0..7, so each load instruction covers 8 splits,
+// and accumulates 8 columns weighted by that split's sum * 2^(m_s - M)
+// (fetched from lane s with a shuffle). The 8 lanes of one chunk are summed
+// at the end, and lanes 0..7 store the row.
+__global__ void __launch_bounds__(256)
+combine_half_kernel(dkv_attn_args a, int splits, const float* __restrict__ part_o,
+                    const float2* __restrict__ part_ml) {
+  const int h = blockIdx.y;
+  const int G = a.q_heads / a.heads;
+  const int R = G * a.nq;
+  const int r = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= R) return;
+  int units = 0;
+  Hist hs;
+  const int active = runtime_plan(a, hs, units, splits);  // partials written (graph replays: fewer)
+  const int64_t base = (int64_t)h * splits * R + r;
+  const int j = lane >> 3, c = lane & 7;
+  const uint4* rows = reinterpret_cast<const uint4*>(part_o);  // 8 chunks of 16 bytes per row
+  float M = -INFINITY, L = 0.f, acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  for (int s0 = 0; s0 < active; s0 += 64) {
+    const int cnt = min(64, active - s0);
+    const float2 ml = lane < cnt ? part_ml[base + (int64_t)(s0 + lane) * R] : make_float2(-INFINITY, 0.f);
+    uint4 raw[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int s = 8 * i + j;
+      raw[i] = s < cnt ? rows[(base + (int64_t)(s0 + s) * R) * 8 + c] : make_uint4(0, 0, 0, 0);
+    }
+    float bm = ml.x;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) bm = fmaxf(bm, __shfl_xor(bm, o));
+    bm = fmaxf(bm, M);
+    if (bm == -INFINITY) continue;  // wave-uniform: every split so far saw no visible key
+    const float f = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - bm);
+    float lsum = ml.y * f;  // also this split's weight of O / sum
+    const float wsplit = lsum;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o);
+    const float f0 = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - bm);
+    L = fmaf(L, f0, lsum);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] *= f0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float w = __shfl(wsplit, 8 * i + j);  // 0 for splits past cnt
+      const uint32_t q[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const _Float16 lo = __builtin_bit_cast(_Float16, (uint16_t)(q[e] & 0xffffu));
+        const _Float16 hi = __builtin_bit_cast(_Float16, (uint16_t)(q[e] >> 16));
+        acc[2 * e] = fmaf((float)lo, w, acc[2 * e]);
+        acc[2 * e + 1] = fmaf((float)hi, w, acc[2 * e + 1]);
+      }
+    }
+    M = bm;
+  }
+#pragma unroll
+  for (int o = 8; o < 64; o <<= 1)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], o);
+  if (j != 0) return;
+  const float inv = 1.f / L;
+  const int gq = r / a.nq, m = r - gq * a.nq;
+  const int64_t off = (int64_t)m * a.out_tok_stride + (int64_t)(h * G + gq) * a.out_head_stride;
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {  // slots 8c + 4 half + [0, 4): 4 consecutive columns
+    const int col = half_column(8 * c + 4 * half);
+    const float v0 = acc[4 * half] * inv, v1 = acc[4 * half + 1] * inv;
+    const float v2 = acc[4 * half + 2] * inv, v3 = acc[4 * half + 3] * inv;
+    if (a.out_dtype == 1)
+      *reinterpret_cast<float4*>(static_cast<float*>(a.out) + off + col) = make_float4(v0, v1, v2, v3);
+    else
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + off + col) =
+          make_uint2(f32_to_bf16_rne(v0) | (f32_to_bf16_rne(v1) << 16), f32_to_bf16_rne(v2) | (f32_to_bf16_rne(v3) << 16));
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -399,8 +488,12 @@ int dkv_attend(const dkv_attn_args* args, void* stream) {
   if (rc) return rc;
   if (p.splits > 1) {
     const int R = (a.q_heads / a.heads) * a.nq;
-    hipLaunchKernelGGL(combine_kernel, dim3((R + 3) / 4, a.heads), dim3(256), 0, s, a, p.splits, part_o,
-                       part_ml);
+    if (p.precision == 1)
+      hipLaunchKernelGGL(combine_kernel, dim3((R + 3) / 4, a.heads), dim3(256), 0, s, a, p.splits, part_o,
+                         part_ml);
+    else
+      hipLaunchKernelGGL(combine_half_kernel, dim3((R + 3) / 4, a.heads), dim3(256), 0, s, a, p.splits, part_o,
+                         part_ml);
   }
   return (int)hipGetLastError();
 }

@@ -98,4 +98,18 @@ int launch_attn_mfma(const dkv_attn_args& a, const Plan& p, float* part_o, float
 constexpr int VEC_ROWS = 64;    // query rows per vector-path workgroup
 constexpr int MFMA_ROWS = 192;  // query rows per MFMA-path workgroup (4 waves x 3 x 16)
 
+// Precision-0 split partials hold O / sum in fp16, 64 values per row (128
+// bytes) in the order the MFMA kernel's lanes store them: the lane of 16-byte
+// chunk c < 4 holds columns 4c + [0, 4) of 16-column blocks 0 and 1, chunk
+// c >= 4 columns 4(c - 4) + [0, 4) of blocks 2 and 3. Slot of column d:
+__host__ __device__ inline int half_slot(int d) {
+  const int db = d >> 4, g = (d >> 2) & 3, e = d & 3;
+  return (db < 2 ? 0 : 32) + 8 * g + 4 * (db & 1) + e;
+}
+// Column of slot i (the inverse of half_slot).
+__host__ __device__ inline int half_column(int i) {
+  const int c = i >> 3, k = i & 7;
+  return 16 * ((c < 4 ? 0 : 2) + (k >> 2)) + 4 * (c & 3) + (k & 3);
+}
+
 }  // namespace dkv

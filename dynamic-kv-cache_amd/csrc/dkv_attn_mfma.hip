@@ -48,6 +48,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int MF_THREADS = 512;
 constexpr int KS = 72;       // LDS row stride, in bf16 elements, of the K and V^T tiles
@@ -510,9 +512,20 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ par
         }
       } else {
         const int64_t base = ((int64_t)h * splits + split) * R + r;
+        if (PREC) {
 #pragma unroll
-        for (int db = 0; db < 4; ++db)
-          __builtin_nontemporal_store(o[db], reinterpret_cast<f32x4*>(part_o + base * D + 16 * db + 4 * g));
+          for (int db = 0; db < 4; ++db)
+            __builtin_nontemporal_store(o[db], reinterpret_cast<f32x4*>(part_o + base * D + 16 * db + 4 * g));
+        } else {  // O / l in fp16, row order of half_slot(): chunks g and 4 + g of the row
+          const float inv = l > 0.f ? 1.f / l : 0.f;
+          _Float16* ph = reinterpret_cast<_Float16*>(part_o) + base * D + 8 * g;
+          const f32x4 a0 = o[0] * inv, a1 = o[1] * inv, a2 = o[2] * inv, a3 = o[3] * inv;
+          __builtin_nontemporal_store(__builtin_convertvector(
+              (f32x8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]}), f16x8), reinterpret_cast<f16x8*>(ph));
+          __builtin_nontemporal_store(__builtin_convertvector(
+              (f32x8{a2[0], a2[1], a2[2], a2[3], a3[0], a3[1], a3[2], a3[3]}), f16x8),
+              reinterpret_cast<f16x8*>(ph + 32));
+        }
         if (g == 0) __builtin_nontemporal_store((f32x2{mm, l}), reinterpret_cast<f32x2*>(part_ml + base));
       }
     }
