@@ -206,24 +206,37 @@ attn_vec_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ part
       else static_cast<uint16_t*>(a.out)[off] = (uint16_t)f32_to_bf16_rne(o);
     } else {
       const int64_t base = ((int64_t)h * splits + split) * R + r;
-      if (PREC)
+      float l = sm[i];
+      if (PREC) {
         __builtin_nontemporal_store(acc[i], part_o + base * D + lane);  // no dirty L2 lines at kernel end
-      else  // O / l in fp16, half_slot() order
-        __builtin_nontemporal_store((_Float16)(sm[i] > 0.f ? acc[i] / sm[i] : 0.f),
-                                    reinterpret_cast<_Float16*>(part_o) + base * D + half_slot(lane));
+      } else {  // O / l in fp16, half_slot() order
+        const float y = l > 0.f ? acc[i] / l : 0.f;
+        _Float16* dst = reinterpret_cast<_Float16*>(part_o) + base * D + half_slot(lane);
+        __builtin_nontemporal_store((_Float16)y, dst);
+        if (__builtin_amdgcn_ballot_w64(fabsf(y) >= 32768.f)) {  // rare: |V| near the fp16 range
+          float amax = fabsf(y);
+#pragma unroll
+          for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+          const int ex = half_partial_exponent(amax);
+          // stored again, scaled (the later store to the same address wins)
+          __builtin_nontemporal_store((_Float16)__builtin_amdgcn_ldexpf(y, -ex), dst);
+          l = half_partial_sum(l, ex);
+        }
+      }
       if (lane == 0) {
         __builtin_nontemporal_store(mx[i], reinterpret_cast<float*>(part_ml + base));
-        __builtin_nontemporal_store(sm[i], reinterpret_cast<float*>(part_ml + base) + 1);
+        __builtin_nontemporal_store(l, reinterpret_cast<float*>(part_ml + base) + 1);
       }
     }
   }
 }
 
-// Log-sum-exp merge of split partials: one wave per query row, lane d owns
-// output column d. The row's split states are read 64 at a time, lane s
-// holding split s: its scale factor 2^(m_s - M) is computed once, on that lane,
-// and every lane takes it with readlane while it accumulates its column, so a
-// row costs one exp per split instead of one per split and column.
+// Precision-1 merge (unnormalized fp32 O partials, 256 bytes per row): one
+// wave per query row. Lane l = 16 j + c reads 16-byte chunk c (columns
+// 4c + [0, 4)) of split s0 + 4 i + j for i = 0..15, so each load instruction
+// covers 4 splits, and accumulates them weighted by 2^(m_s - M), computed once
+// on lane s and fetched with a shuffle. The 4 lanes of one chunk are summed at
+// the end, and lanes 0..15 store the row.
 __global__ void __launch_bounds__(256)
 combine_kernel(dkv_attn_args a, int splits, const float* __restrict__ part_o,
                const float2* __restrict__ part_ml) {
@@ -237,10 +250,18 @@ combine_kernel(dkv_attn_args a, int splits, const float* __restrict__ part_o,
   Hist hs;
   const int active = runtime_plan(a, hs, units, splits);  // partials written (graph replays: fewer)
   const int64_t base = (int64_t)h * splits * R + r;
-  float M = -INFINITY, L = 0.f, O = 0.f;
+  const int j = lane >> 4, c = lane & 15;
+  const float4* rows = reinterpret_cast<const float4*>(part_o);  // 16 chunks of 16 bytes per row
+  float M = -INFINITY, L = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
   for (int s0 = 0; s0 < active; s0 += 64) {
     const int cnt = min(64, active - s0);
     const float2 ml = lane < cnt ? part_ml[base + (int64_t)(s0 + lane) * R] : make_float2(-INFINITY, 0.f);
+    float4 raw[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int sp = 4 * i + j;
+      raw[i] = sp < cnt ? rows[(base + (int64_t)(s0 + sp) * R) * 16 + c] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     float bm = ml.x;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) bm = fmaxf(bm, __shfl_xor(bm, o));
@@ -252,22 +273,32 @@ combine_kernel(dkv_attn_args a, int splits, const float* __restrict__ part_o,
     for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o);
     const float f0 = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - bm);
     L = fmaf(L, f0, lsum);
-    O *= f0;
-    // All of the chunk's loads are issued before the first use.
-    const float* po = part_o + (base + (int64_t)s0 * R) * D + lane;
-    float o[64];
 #pragma unroll
-    for (int i = 0; i < 64; ++i) o[i] = i < cnt ? po[(int64_t)i * R * D] : 0.f;
+    for (int e = 0; e < 4; ++e) acc[e] *= f0;
 #pragma unroll
-    for (int i = 0; i < 64; ++i)
-      O = fmaf(o[i], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), i)), O);
+    for (int i = 0; i < 16; ++i) {
+      const float w = __shfl(f, 4 * i + j);  // 0 for splits past cnt
+      acc[0] = fmaf(raw[i].x, w, acc[0]);
+      acc[1] = fmaf(raw[i].y, w, acc[1]);
+      acc[2] = fmaf(raw[i].z, w, acc[2]);
+      acc[3] = fmaf(raw[i].w, w, acc[3]);
+    }
     M = bm;
   }
-  const float out = O / L;
-  const int g = r / a.nq, m = r - g * a.nq;
-  const int64_t off = (int64_t)m * a.out_tok_stride + (int64_t)(h * G + g) * a.out_head_stride + lane;
-  if (a.out_dtype == 1) static_cast<float*>(a.out)[off] = out;
-  else static_cast<uint16_t*>(a.out)[off] = (uint16_t)f32_to_bf16_rne(out);
+#pragma unroll
+  for (int o = 16; o < 64; o <<= 1)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] += __shfl_xor(acc[e], o);
+  if (j != 0) return;
+  const float inv = 1.f / L;
+  const float v0 = acc[0] * inv, v1 = acc[1] * inv, v2 = acc[2] * inv, v3 = acc[3] * inv;
+  const int gq = r / a.nq, m = r - gq * a.nq;
+  const int64_t off = (int64_t)m * a.out_tok_stride + (int64_t)(h * G + gq) * a.out_head_stride + 4 * c;
+  if (a.out_dtype == 1)
+    *reinterpret_cast<float4*>(static_cast<float*>(a.out) + off) = make_float4(v0, v1, v2, v3);
+  else
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + off) =
+        make_uint2(f32_to_bf16_rne(v0) | (f32_to_bf16_rne(v1) << 16), f32_to_bf16_rne(v2) | (f32_to_bf16_rne(v3) << 16));
 }
 
 // Precision-0 merge (fp16 O / sum partials, 128 bytes per row in half_slot()
@@ -309,8 +340,9 @@ combine_half_kernel(dkv_attn_args a, int splits, const float* __restrict__ part_
     bm = fmaxf(bm, M);
     if (bm == -INFINITY) continue;  // wave-uniform: every split so far saw no visible key
     const float f = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - bm);
-    float lsum = ml.y * f;  // also this split's weight of O / sum
-    const float wsplit = lsum;
+    int ex;
+    float lsum = half_partial_decode(ml.y, ex) * f;
+    const float wsplit = ex ? __builtin_amdgcn_ldexpf(lsum, ex) : lsum;  // weight of the stored O / sum / 2^ex
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o);
     const float f0 = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - bm);
@@ -403,6 +435,10 @@ static int check_args(const dkv_attn_args& a) {
   if (!a16(a.q) || !a16(a.k_new) || !a16(a.v_new) || (a.q_head_stride & 7) || (a.q_tok_stride & 7) ||
       (a.kn_head_stride & 7) || (a.kn_tok_stride & 7) || (a.vn_head_stride & 7) || (a.vn_tok_stride & 7)) {
     set_error("dkv_attend: Q/K/V must be 16-byte aligned with strides that are multiples of 8 elements");
+    return DKV_EINVAL;
+  }
+  if (!a16(a.out) || (a.out_tok_stride & 3) || (a.out_head_stride & 3)) {  // rows are stored 4 columns at a time
+    set_error("dkv_attend: out must be 16-byte aligned with strides that are multiples of 4 elements");
     return DKV_EINVAL;
   }
   return 0;

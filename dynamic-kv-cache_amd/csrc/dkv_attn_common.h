@@ -112,4 +112,25 @@ __host__ __device__ inline int half_column(int i) {
   return 16 * ((c < 4 ? 0 : 2) + (k >> 2)) + 4 * (c & 3) + (k & 3);
 }
 
+// fp16 partials hold O / sum, bounded by the row's largest |V|, which can pass
+// the fp16 range (65504) where bf16 K/V do not. A row whose largest |O / sum|
+// reaches 2^15 is stored scaled by 2^-e (e >= 1, the largest stored value then
+// below 2^15), and its sum is stored with the sign bit set and e in the low 8
+// bits of its mantissa (a relative change below 2^-15); every other row keeps
+// e = 0 and its sum as is.
+__device__ __forceinline__ int half_partial_exponent(float amax) {
+  if (!(amax >= 32768.f)) return 0;  // NaN stays unscaled
+  return (int)((__float_as_uint(amax) >> 23) & 0xffu) - 127 - 14;
+}
+__device__ __forceinline__ float half_partial_sum(float l, int e) {
+  return e ? __uint_as_float(0x80000000u | (__float_as_uint(l) & 0x7fffff00u) | (uint32_t)e) : l;
+}
+// The stored sum of a row and its exponent e (the row's values are O / sum / 2^e).
+__device__ __forceinline__ float half_partial_decode(float stored, int& e) {
+  const uint32_t b = __float_as_uint(stored);
+  const bool scaled = b >> 31;
+  e = scaled ? (int)(b & 0xffu) : 0;
+  return scaled ? __uint_as_float(b & 0x7fffff00u) : stored;
+}
+
 }  // namespace dkv

@@ -490,7 +490,7 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ par
       const float mm = fmaxf(m_run[nb], o1.x);
       const float f0 = mm == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[nb] - mm);
       const float f1 = mm == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(o1.x - mm);
-      const float l = lsum[nb] * f0 + o1.y * f1;
+      float l = lsum[nb] * f0 + o1.y * f1;
       const int r = rg * MFMA_ROWS + lr;
       f32x4 o[4];
 #pragma unroll
@@ -520,11 +520,30 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ par
           const float inv = l > 0.f ? 1.f / l : 0.f;
           _Float16* ph = reinterpret_cast<_Float16*>(part_o) + base * D + 8 * g;
           const f32x4 a0 = o[0] * inv, a1 = o[1] * inv, a2 = o[2] * inv, a3 = o[3] * inv;
-          __builtin_nontemporal_store(__builtin_convertvector(
-              (f32x8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]}), f16x8), reinterpret_cast<f16x8*>(ph));
-          __builtin_nontemporal_store(__builtin_convertvector(
-              (f32x8{a2[0], a2[1], a2[2], a2[3], a3[0], a3[1], a3[2], a3[3]}), f16x8),
-              reinterpret_cast<f16x8*>(ph + 32));
+          auto store_row = [&](const f32x4& b0, const f32x4& b1, const f32x4& b2, const f32x4& b3) {
+            __builtin_nontemporal_store(__builtin_convertvector(
+                (f32x8{b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]}), f16x8), reinterpret_cast<f16x8*>(ph));
+            __builtin_nontemporal_store(__builtin_convertvector(
+                (f32x8{b2[0], b2[1], b2[2], b2[3], b3[0], b3[1], b3[2], b3[3]}), f16x8),
+                reinterpret_cast<f16x8*>(ph + 32));
+          };
+          store_row(a0, a1, a2, a3);
+          float amax = 0.f;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(a0[e]), fabsf(a1[e])), fmaxf(fabsf(a2[e]), fabsf(a3[e]))));
+          // Rare (|V| near the fp16 range, where the stores above hold inf): the
+          // row's maximum over its 4 lane groups (lanes col + 16 g, all active
+          // since they share r) picks the exponent, and the lane stores the row
+          // again, scaled (the later store to the same address wins).
+          if (__builtin_amdgcn_ballot_w64(amax >= 32768.f)) {
+            const int ex = half_partial_exponent(group_max(amax));
+            if (ex) {
+              const float sc = __builtin_amdgcn_ldexpf(1.f, -ex);
+              store_row(a0 * sc, a1 * sc, a2 * sc, a3 * sc);
+              l = half_partial_sum(l, ex);
+            }
+          }
         }
         if (g == 0) __builtin_nontemporal_store((f32x2{mm, l}), reinterpret_cast<f32x2*>(part_ml + base));
       }

@@ -173,7 +173,9 @@ int64_t dkv_attend_workspace_bytes(const dkv_attn_args* args);
 /* Fused packed-history causal GQA attention. Replaces GPUCache.attend's
  * packed_attention launch (src/gpu_cache.py:96-104, src/gpu_kernels.py:71-105).
  * Output rows are written to out + m*out_tok_stride + qh*out_head_stride
- * (elements), the reference's [1, nq, q_heads, 64] layout when contiguous. */
+ * (elements), the reference's [1, nq, q_heads, 64] layout when contiguous.
+ * Q, K and V must be 16-byte aligned with strides in multiples of 8 elements;
+ * out 16-byte aligned with strides in multiples of 4 elements. */
 int dkv_attend(const dkv_attn_args* args, void* stream);
 
 /* Copy one segment out of the arena into the reference's PackedTensor buffers

@@ -125,6 +125,8 @@ def attn(**kw):
     (dict(out_dtype=2), 'out_dtype'),
     (dict(q_tok_stride=60), 'aligned'),
     (dict(n_tiles=3), 'null'),
+    (dict(out=4096 + 8), 'out must be'),
+    (dict(out_tok_stride=15 * 64 + 2), 'out must be'),
 ])
 def test_attend_rejects_bad_arguments(kw, msg):
     lib = _lib.load()

@@ -195,6 +195,31 @@ def test_split_counts_agree(cuda, splits, path):
 
 
 @pytest.mark.parametrize('path', PATHS)
+@pytest.mark.parametrize('splits', [0, 1000])
+def test_bf16_split_partials_keep_large_values_finite(cuda, splits, path):
+    """bf16 precision stores split partials O / sum in fp16 (largest finite 65504). Scaling V by
+    2^20 (|V| up to ~1e8, finite in bf16) scales every product exactly, and the reference stays
+    finite: so must this, at 2^20 times the unscaled output. The partial store rescales rows
+    past 2^15 by a power of two and the combine undoes it; without that the row is inf. Bound:
+    2^-12 relative for the fp16 rounding of the partials, plus 2^-13 of the largest output: the
+    stored sum's low 8 mantissa bits carry the exponent, a 2^-15 relative change of that split's
+    weight, which moves an element by up to 2^-14 of its row's range (far below the bf16
+    rounding of p that this precision already applies to every weight)."""
+    announce(f'attention large V splits={splits} path={path}')
+    case = frame_chunk_case(2048, seed=5)
+    outs = []
+    for scale in (1.0, 2.0 ** 20):
+        big = dict(case, v_hist=case['v_hist'] * scale, v_new=case['v_new'] * scale)
+        c, _, _ = build(big, cuda)
+        outs.append(run(c, big, cuda, torch.float32, splits=splits, path=path, precision='bf16') / scale)
+    small, large = outs
+    assert torch.isfinite(large).all()
+    assert small.abs().max().item() > 1.0  # outlier channels: the scaled rows pass 2^15
+    bound = small.abs() * 2.0 ** -12 + small.abs().max() * 2.0 ** -13
+    assert ((large - small).abs() <= bound).all(), (large - small).abs().max().item()
+
+
+@pytest.mark.parametrize('path', PATHS)
 @pytest.mark.parametrize('bits', [4, 8])
 def test_candidates_block_diagonal(cuda, bits, path):
     announce(f'attention candidates bits={bits} path={path}')
