@@ -195,6 +195,26 @@ def test_split_counts_agree(cuda, splits, path):
 
 
 @pytest.mark.parametrize('path', PATHS)
+@pytest.mark.parametrize('precision', ['fp32', 'bf16'])
+def test_more_splits_than_one_merge_pass(cuda, precision, path):
+    """128 splits (one per 64-key unit at past 8128): the combine kernels take a row's splits 64 at
+    a time and rescale their running (max, sum, O) between the two passes. Same bounds as the
+    single-pass cases: fp32 within 1e-3 of the fp64 oracle, bf16 within 2e-2 of the emulated
+    reference plus its own 32-vs-64-key block sensitivity."""
+    announce(f'attention 128 splits precision={precision} path={path}')
+    case = frame_chunk_case(8128, seed=9)
+    c, dk, dv = build(case, cuda)
+    got = run(c, case, cuda, torch.float32, splits=1000, path=path, precision=precision)
+    if precision == 'fp32':
+        err = (got - oracle_out(case, dk, dv)).abs().max().item()
+        assert err <= 1e-3, err
+    else:
+        err = (got - semantics_out(case, dk, dv, None, torch.float32)).abs().max().item()
+        tol = 2e-2 + block_sensitivity(case, dk, dv)
+        assert err <= tol, (err, tol)
+
+
+@pytest.mark.parametrize('path', PATHS)
 @pytest.mark.parametrize('splits', [0, 1000])
 def test_bf16_split_partials_keep_large_values_finite(cuda, splits, path):
     """bf16 precision stores split partials O / sum in fp16 (largest finite 65504). Scaling V by
