@@ -91,32 +91,54 @@ __global__ void __launch_bounds__(64 * WAVES) linear_kernel(const LinearArgs a) 
   }
 
   // Every load of this wave's pairs (the host guarantees CH * WAVES >= kp) is
-  // issued before the first MFMA; p < kp is uniform over the wave.
-  Op8 xa[CH][2][RB], wa[CH][2][NB];
+  // issued before the first MFMA. With the RMSNorm prologue the x rows and
+  // the norm weight go first, unconditionally (a pair past kp loads pair
+  // kp - 1 and is skipped below, so the loads form one straight-line block
+  // whose uses wait for exactly what they need): the prologue waits only for
+  // them and normalizes while the weight tiles, which come from HBM, are in
+  // flight. Without it the first MFMA needs both, and pairs past kp (p < kp is
+  // uniform over the wave) load nothing.
+  Op8 xa[CH][2][RB], wa[CH][2][NB], gn[NORM ? CH : 1][2];
+  if constexpr (NORM) {
 #pragma unroll
-  for (int i = 0; i < CH; ++i) {
-    const int p = wave + WAVES * i;
-    if (p < a.kp) {
+    for (int i = 0; i < CH; ++i) {
+      const int p = min(wave + WAVES * i, a.kp - 1);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int k = 64 * p + 32 * h;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) xa[i][h][rb].u = *reinterpret_cast<const u32x4*>(xrow[rb] + k);
+        gn[i][h].u = *reinterpret_cast<const u32x4*>(a.norm + k + 8 * g);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int p = min(wave + WAVES * i, a.kp - 1);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int k = 64 * p + 32 * h;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) wa[i][h][nb].u = *reinterpret_cast<const u32x4*>(wrow[nb] + k);
+      }
+    }
+  } else {
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) xa[i][h][rb].u = *reinterpret_cast<const u32x4*>(xrow[rb] + k);
+    for (int i = 0; i < CH; ++i) {
+      const int p = wave + WAVES * i;
+      if (p < a.kp) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int k = 64 * p + 32 * h;
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) wa[i][h][nb].u = *reinterpret_cast<const u32x4*>(wrow[nb] + k);
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb) xa[i][h][rb].u = *reinterpret_cast<const u32x4*>(xrow[rb] + k);
+        }
       }
     }
   }
   if (NORM) {
     __shared__ float ssum[WAVES][RB][16];
-    Op8 gn[CH][2];
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const int p = wave + WAVES * i;
-      if (p < a.kp)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) gn[i][h].u = *reinterpret_cast<const u32x4*>(a.norm + 64 * p + 32 * h + 8 * g);
-    }
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       float ss = 0.f;
