@@ -472,7 +472,7 @@ static Plan make_plan(const dkv_attn_args& a) {
   if (splits < 1) splits = 1;
   p.splits = splits;
   if (splits > 1) {
-    p.part_o_bytes = (int64_t)a.heads * splits * R * D * 4;
+    p.part_o_bytes = (int64_t)a.heads * splits * R * D * (p.precision ? 4 : 2);  // fp32 O or fp16 O / sum
     p.part_ml_bytes = (int64_t)a.heads * splits * R * 8;
   } else {
     p.part_o_bytes = p.part_ml_bytes = 0;

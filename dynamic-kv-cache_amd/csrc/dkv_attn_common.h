@@ -77,8 +77,9 @@ __device__ __forceinline__ int chunk_seg_start(const dkv_attn_args& a, int j) {
   return start;
 }
 
-// Workspace of a split call: partial outputs [heads, splits, R, 64] fp32, then
-// partial (max, sum) [heads, splits, R] float2.
+// Workspace of a split call: partial outputs [heads, splits, R, 64] (fp32 O
+// for precision 1, fp16 O / sum for precision 0), then partial (max, sum)
+// [heads, splits, R] float2.
 struct Plan {
   int path;       // 1 vector, 2 MFMA
   int precision;  // 0 bf16 operands (reference rounding), 1 fp32-accurate

@@ -153,6 +153,18 @@ def test_attend_demands_workspace_when_split():
     assert 'workspace' in lib.dkv_last_error().decode()
 
 
+def test_attend_workspace_matches_the_partial_format():
+    """Per split row: 64 fp16 O / sum values + (max, sum) in bf16 precision, 64 fp32 O + (max, sum)
+    in fp32 precision."""
+    lib = _lib.load()
+    need = {}
+    for precision in (0, 1):
+        a = attn(past=4096, n_tiles=64, arena=4096, tiles=4096, precision=precision)
+        need[precision] = lib.dkv_attend_workspace_bytes(ctypes.byref(a))
+    rows = need[1] // (64 * 4 + 8)
+    assert rows > 0 and need[1] == rows * (64 * 4 + 8) and need[0] == rows * (64 * 2 + 8)
+
+
 def test_pack_validate_checks_every_job_of_a_host_table():
     lib = _lib.load()
     good = [job(seg_offset=0), job(seg_offset=4096, layer=1)]
