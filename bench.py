@@ -24,6 +24,7 @@ sys.path.insert(0, REPO)
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 LAYERS, HEADS, Q_HEADS, TILE = 32, 5, 15, 64
+PIPELINE = int(os.environ.get('DKV_PIPELINE', '4'))  # frames per pipelined graph replay in the e2e run
 
 
 def parse():
@@ -272,8 +273,10 @@ def bench_e2e(frame_counts=(16, 64, 96), reps=2):
         frames = [emb[i:i + 1] for i in range(nf)]
         bits = bit_schedule(nf, nf)
         best = {}
-        for graphs in (False, True):
-            dec.graphs = graphs
+        # eager launches; graph replays of consecutive frames pipelined in groups (the default);
+        # graph replays one frame at a time
+        for mode, graphs, pipeline in (('eager', False, 1), ('graph', True, PIPELINE), ('graph1', True, 1)):
+            dec.graphs, dec.pipeline = graphs, pipeline
             for proto in ('forks', 'batched'):
                 times = []
                 for _ in range(reps + 1):  # the first request warms up kernels, GEMM selection, the capture
@@ -288,16 +291,16 @@ def bench_e2e(frame_counts=(16, 64, 96), reps=2):
                     torch.cuda.synchronize()
                     times.append(time.perf_counter() - t0)
                     del cache
-                best[(graphs, proto)] = min(times[1:])
+                best[(mode, proto)] = min(times[1:])
         r = out[f'frames_{nf}'] = dict(tokens=16 + 64 * nf + 24 + sum(c.shape[1] for c in cands))
-        for (graphs, proto), t in best.items():
-            tag = f"{'graph' if graphs else 'eager'}_{proto}"
-            r[f'frames_per_s_{tag}'] = round(nf / t, 2)
-            r[f'request_s_{tag}'] = round(t, 4)
+        for (mode, proto), t in best.items():
+            r[f'frames_per_s_{mode}_{proto}'] = round(nf / t, 2)
+            r[f'request_s_{mode}_{proto}'] = round(t, 4)
         print(f"# e2e {nf} frames: eager {r['frames_per_s_eager_forks']} / {r['frames_per_s_eager_batched']}, "
-              f"graph {r['frames_per_s_graph_forks']} / {r['frames_per_s_graph_batched']} frames/s (forks / batched)",
-              flush=True)
-    dec.graphs = False
+              f"graph {r['frames_per_s_graph_forks']} / {r['frames_per_s_graph_batched']}, "
+              f"graph frame by frame {r['frames_per_s_graph1_forks']} / {r['frames_per_s_graph1_batched']} "
+              f"frames/s (forks / batched)", flush=True)
+    dec.graphs, dec.pipeline = False, PIPELINE
     return out
 
 

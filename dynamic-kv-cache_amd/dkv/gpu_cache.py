@@ -11,9 +11,9 @@ hand-written HIP kernels reached through libdkv's C ABI (include/dkv.h).
 """
 import bisect
 import ctypes
-import struct
 import types
 
+import numpy as np
 import torch
 import torch.nn.functional as F
 
@@ -625,9 +625,11 @@ class GraphSteps:
     {past, n_tiles} pair every attention launch reads (dkv_attn_args.step). step() does the host
     bookkeeping of one chunk and uploads the buffer through a ring of pinned host copies, so the
     host can prepare step i+1 while the GPU still runs step i. The K/V pointers of the jobs are
-    those append() saw while the graph was captured (they are fixed for a captured graph).
+    those append() saw while the graph was captured (they are fixed for a captured graph): a
+    ring slot gets them once, and a step rewrites only the fields every layer's job shares.
     """
     RING = 4
+    JOB = np.dtype(_lib.PackJob)
 
     def __init__(self, cache, chunk):
         self.cache, self.chunk = cache, chunk
@@ -638,7 +640,10 @@ class GraphSteps:
             self.ring = [(torch.zeros(self.nbytes, dtype=torch.uint8, pin_memory=True), None)
                          for _ in range(self.RING)]
         self.slot = 0
+        self.views = [self._view(host) for host, _ in self.ring]
         self.kv = [None] * cache.layers  # (k, v) views append() recorded, kept alive with the graph
+        self.kv_version = 0  # bumped whenever append() records a view
+        self.slot_kv = [-1] * self.RING  # kv_version each slot's pointer fields were written with
         self.state = None  # (past, segment, write_tiles) of the current step
         # Launch bounds: the largest history a chunk can attend to in this cache.
         self.past_bound = cache.capacity - chunk
@@ -674,25 +679,40 @@ class GraphSteps:
         self.upload()
         return past
 
+    def _view(self, host):
+        """(jobs, tail) numpy views of a pinned ring buffer: the per-layer PackJob array, then the
+        {past, n_tiles} int32 pair."""
+        raw = host.numpy()
+        split = self.cache.layers * self.job_bytes
+        return raw[:split].view(self.JOB), raw[split:split + 8].view(np.int32)
+
     def upload(self):
         """Writes the current step's jobs and bounds to the device buffer (async, stream-ordered)."""
         c, n = self.cache, self.chunk
         past, seg, write = self.state
-        jobs = (_lib.PackJob * c.layers)()
-        for l in range(c.layers):
-            kv = self.kv[l]
-            kp, vp, ks, vs = (kv[0].data_ptr(), kv[1].data_ptr(), kv[0].stride(), kv[1].stride()) if kv else \
-                (0, 0, (0, 0, 0, 0), (0, 0, 0, 0))
-            jobs[l] = _lib.PackJob(kp, vp, ks[1], ks[2], vs[1], vs[2], seg.offset, seg.rows, seg.start,
-                                   past - seg.start, n, l, seg.bits, seg.tile0, write if l == 0 else 0)
-        if all(kv is not None for kv in self.kv):
-            _lib.check(_lib.load().dkv_pack_validate(ctypes.addressof(jobs), c.layers, c.arena_bytes, c.layers,
-                                                     c.heads), 'dkv_pack_validate')
         host, event = self.ring[self.slot]
         if event is not None:
             event.synchronize()  # that slot's previous copy has been consumed
-        raw = bytes(jobs) + struct.pack('<ii', past, c._tiles_before(past))
-        host.copy_(torch.frombuffer(bytearray(raw), dtype=torch.uint8))
+        jobs, tail = self.views[self.slot]
+        if self.slot_kv[self.slot] != self.kv_version:
+            for l, kv in enumerate(self.kv):
+                kp, vp, ks, vs = (kv[0].data_ptr(), kv[1].data_ptr(), kv[0].stride(), kv[1].stride()) if kv else \
+                    (0, 0, (0, 0, 0, 0), (0, 0, 0, 0))
+                jobs[l] = (kp, vp, ks[1], ks[2], vs[1], vs[2], 0, 0, 0, 0, 0, l, 0, 0, 0)
+            self.slot_kv[self.slot] = self.kv_version
+        jobs['seg_offset'] = seg.offset
+        jobs['seg_rows'] = seg.rows
+        jobs['seg_token_start'] = seg.start
+        jobs['row0'] = past - seg.start
+        jobs['n'] = n
+        jobs['bits'] = seg.bits
+        jobs['tile_index0'] = seg.tile0
+        jobs['write_tiles'] = 0
+        jobs['write_tiles'][0] = write  # layer 0's job writes the segment's tile descriptors
+        tail[0], tail[1] = past, c._tiles_before(past)
+        if all(kv is not None for kv in self.kv):
+            _lib.check(_lib.load().dkv_pack_validate(host.data_ptr(), c.layers, c.arena_bytes, c.layers, c.heads),
+                       'dkv_pack_validate')
         self.dev.copy_(host, non_blocking=True)
         event = torch.cuda.Event()
         event.record()
@@ -707,6 +727,7 @@ class GraphSteps:
             raise ValueError(f'graph steps were set up for {self.chunk}-token chunks, got {k.shape[-2]}')
         k, v = c._kv_view(k), c._kv_view(v)
         self.kv[layer] = (k, v)
+        self.kv_version += 1
         _lib.check(_lib.load().dkv_pack_batch(self.dev.data_ptr() + layer * self.job_bytes, 1, self.chunk,
                                               c.arena.data_ptr(), c.arena_bytes, c.tiles.data_ptr(), c.layers,
                                               c.heads, _lib.stream_handle(c.device)), 'dkv_pack_batch')
@@ -719,6 +740,7 @@ class GraphSteps:
         if qkv.shape[0] != self.chunk:
             raise ValueError(f'graph steps were set up for {self.chunk}-token chunks, got {qkv.shape[0]}')
         self.kv[layer] = (k, v)
+        self.kv_version += 1
         _lib.check(_lib.load().dkv_rope_pack(
             qkv.data_ptr(), qkv.stride(0), cos.data_ptr(), sin.data_ptr(), cos.stride(0), self.chunk, q_heads,
             q.data_ptr(), k.data_ptr(), v.data_ptr(), self.dev.data_ptr() + layer * self.job_bytes, 1,

@@ -45,17 +45,19 @@ def build_decoder(layers=32, hidden=960, heads=15, kv_heads=5, intermediate=2560
 class StreamingDecoder:
     """Frame-by-frame ingestion into a GPUCache and candidate scoring (src/streaming.py:89-237)."""
 
-    def __init__(self, model, fused_ops=True, precision='bf16', graphs=False):
+    def __init__(self, model, fused_ops=True, precision='bf16', graphs=False, pipeline=4):
         self.model = model
         self.text = model.model
         self.config = model.config
         self.precision = precision
         self.graphs = graphs
+        self.pipeline = pipeline
         self.ops_state = {'enabled': fused_ops}
         install_fused_ops(self.text, self.ops_state)
         install_packed_attention(model)
         self._cache = None  # reused across requests when graphs=True (a captured graph records its buffers)
         self._graphs = {}  # chunk length -> captured forward of that length on self._cache
+        self._group_graphs = {}  # (chunk length, k) -> captured forwards of k consecutive chunks (pipelined)
 
     @property
     def device(self):
@@ -88,7 +90,11 @@ class StreamingDecoder:
 
         With graphs=True the frames after the first run as replays of one captured HIP graph of the
         whole decoder forward (the cache's launches read their step parameters from the device), on
-        a cache the decoder keeps and resets between requests.
+        a cache the decoder keeps and resets between requests. With pipeline=k > 1 as well, k
+        consecutive frames replay one graph of their k forwards in which frame i + 1's layer l
+        waits only for frame i's layer l (the K/V it attends to) and its own layer l - 1: each
+        forward runs one layer behind the one before it, on its own stream. The launches and the
+        data are those of one frame after the other; the GPU overlaps them.
         """
         if len(frames) != len(bits):
             raise ValueError('one bit width per frame')
@@ -100,16 +106,28 @@ class StreamingDecoder:
         # The first request's prefix and first frame run eagerly (they warm up the library paths
         # a capture records); after that every chunk replays the captured forward of its length
         # (captured on first use).
-        if graphed and self._graphs:
+        warm = bool(self._graphs or self._group_graphs)
+        if graphed and warm:
             self._graph_chunk(cache, self.text.get_input_embeddings()(prefix_ids.to(self.device)))
         else:
             self.forward(cache, ids=prefix_ids)
-        for i, (emb, b) in enumerate(zip(frames, bits)):
+        i = 0
+        while i < len(frames):
+            emb, b = frames[i], bits[i]
+            replay = graphed and (i > 0 or warm)
+            k = 1
+            while k < self.pipeline and i + k < len(frames) and frames[i + k].shape[1] == emb.shape[1]:
+                k += 1
+            if replay and k > 1:
+                self._graph_group(cache, frames[i:i + k], bits[i:i + k], i)
+                i += k
+                continue
             cache.select(b, i)
-            if graphed and (i > 0 or self._graphs):
+            if replay:
                 self._graph_chunk(cache, emb)
             else:
                 self.forward(cache, embeddings=emb)
+            i += 1
         cache.select(16, -1)
         if len(set(cache.seen)) != 1:
             raise RuntimeError('Decoder layers disagree about the cache length')
@@ -118,7 +136,7 @@ class StreamingDecoder:
     def _reused_cache(self, total):
         if self._cache is None or self._cache.capacity < total:
             self._cache = self.create_cache(max(total, 8192))
-            self._graphs = {}  # a captured graph records the old cache's buffers
+            self._graphs, self._group_graphs = {}, {}  # a captured graph records the old cache's buffers
         else:
             self._cache.reset()
         return self._cache
@@ -157,6 +175,80 @@ class StreamingDecoder:
         finally:
             cache.end_graph_steps()
         self._graphs[chunk] = dict(chunk=chunk, graph=graph, steps=steps, emb=static_emb, pos=pos, arange=arange)
+
+    def _group_steps(self, cache, chunk, bits, frame, steps):
+        """Host bookkeeping of frames frame .. frame + k - 1 (one GraphSteps each, since their
+        forwards run at once); returns their history lengths and the GraphSteps."""
+        past, out = [], []
+        for j, st in enumerate(steps):
+            cache.select(bits[j], frame + j)
+            cache.begin_graph_steps(chunk, q_heads=None if st else self.config.num_attention_heads, steps=st)
+            try:
+                past.append(cache.graph_step())
+            finally:
+                out.append(cache.end_graph_steps())
+        return past, out
+
+    def _graph_group(self, cache, embs, bits, frame):
+        """k consecutive frames as one replay of their pipelined forwards (captured on first use)."""
+        chunk, k = embs[0].shape[1], len(embs)
+        fg = self._group_graphs.get((chunk, k))
+        if fg is None:
+            self._capture_group(cache, embs, bits, frame)
+            return
+        past, _ = self._group_steps(cache, chunk, bits, frame, fg['steps'])
+        for j in range(k):
+            fg['emb'][j].copy_(embs[j])
+            torch.add(fg['arange'], past[j], out=fg['pos'][j][0])
+        fg['graph'].replay()
+
+    def _capture_group(self, cache, embs, bits, frame):
+        chunk, k = embs[0].shape[1], len(embs)
+        static_emb = [e.clone() for e in embs]
+        arange = torch.arange(chunk, device=self.device)
+        pos = [torch.empty((1, chunk), dtype=torch.long, device=self.device) for _ in range(k)]
+        past, steps = self._group_steps(cache, chunk, bits, frame, [None] * k)
+        for j in range(k):
+            torch.add(arange, past[j], out=pos[j][0])
+        layers = self.text.layers
+        done = [[torch.cuda.Event() for _ in layers] for _ in range(k - 1)]  # frame j's layer l has finished
+        streams = [torch.cuda.Stream(device=self.device) for _ in range(k - 1)]
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        hooks = []
+        try:
+            with torch.cuda.graph(graph):
+                first = torch.cuda.current_stream()
+                for st in streams:
+                    st.wait_stream(first)  # the fork: the other forwards join the capture here
+                for j in range(k):
+                    stream = first if j == 0 else streams[j - 1]
+                    if j > 0:  # layer l after the previous frame's layer l
+                        hooks += [m.register_forward_pre_hook(
+                            lambda mod, inp, l=l, ev=done[j - 1], st=stream: st.wait_event(ev[l]))
+                            for l, m in enumerate(layers)]
+                    if j < k - 1:
+                        hooks += [m.register_forward_hook(lambda mod, inp, out, l=l, ev=done[j]: ev[l].record())
+                                  for l, m in enumerate(layers)]
+                    cache.begin_graph_steps(chunk, steps=steps[j])
+                    with torch.cuda.stream(stream):
+                        self.text(inputs_embeds=static_emb[j], past_key_values=cache, use_cache=True,
+                                  position_ids=pos[j], attention_mask=None, return_dict=True)
+                    cache.end_graph_steps()
+                    for h in hooks:
+                        h.remove()
+                    hooks = []
+                for st in streams:
+                    first.wait_stream(st)
+        finally:
+            for h in hooks:
+                h.remove()
+            cache.end_graph_steps()
+        for st in steps:
+            st.upload()  # the jobs now carry the K/V addresses recorded in the graph
+        graph.replay()
+        self._group_graphs[(chunk, k)] = dict(graph=graph, steps=steps, emb=static_emb, pos=pos, arange=arange,
+                                              events=done, streams=streams)
 
     @staticmethod
     def _mean_loglik(logits, targets):

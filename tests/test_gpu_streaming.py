@@ -93,15 +93,17 @@ def test_mixed_width_ingest_tracks_the_schedule(cuda):
     assert torch.isfinite(logits).all()
 
 
-def test_graph_replayed_ingest_matches_eager(cuda):
-    """Frames 2..n replay one captured HIP graph of the decoder forward (launches read their step
+@pytest.mark.parametrize('pipeline', [1, 2, 3])
+def test_graph_replayed_ingest_matches_eager(cuda, pipeline):
+    """Frames 2..n replay captured HIP graphs of the decoder forward (launches read their step
     parameters from the device, and the attention runs the splits the host plan would choose for
-    the current history). The cache bookkeeping, the packed bytes and the logits must equal the
-    eager ingest's exactly, and a second request that reuses the captured graph on the reset
-    cache must reproduce the first bit for bit."""
-    announce('streaming: graph-replayed ingest vs eager, two requests')
+    the current history); with pipeline=k, k consecutive frames replay one graph of their
+    forwards, each a layer behind the one before on its own stream. The cache bookkeeping, the
+    packed bytes and the logits must equal the eager ingest's exactly, and a second request that
+    reuses the captured graphs on the reset cache must reproduce the first bit for bit."""
+    announce(f'streaming: graph-replayed ingest vs eager, two requests, pipeline={pipeline}')
     model = build_decoder(**SMALL, seed=12)
-    dec = StreamingDecoder(model, precision='fp32')
+    dec = StreamingDecoder(model, precision='fp32', pipeline=pipeline)
     g = torch.Generator().manual_seed(13)
     prefix = torch.randint(0, 512, (1, 16), generator=g)
     question = torch.randint(0, 512, (1, 24), generator=g)
@@ -117,7 +119,10 @@ def test_graph_replayed_ingest_matches_eager(cuda):
     eager_cache, eager = run()
     dec.graphs = True
     graph_cache, first = run()
-    assert 64 in dec._graphs and graph_cache is dec._cache
+    assert graph_cache is dec._cache
+    # frames 1-5: alone; as pairs 1-2, 3-4 and frame 5 alone; as groups 1-3 and 4-5
+    expect = {1: ({64}, set()), 2: ({64}, {(64, 2)}), 3: (set(), {(64, 3), (64, 2)})}[pipeline]
+    assert (set(dec._graphs), set(dec._group_graphs)) == expect
     assert graph_cache.plan == eager_cache.plan and graph_cache.seen == eager_cache.seen
     assert [s.frame for s in graph_cache.segments] == [s.frame for s in eager_cache.segments]
     assert graph_cache.accounting()['precision_token_counts'] == eager_cache.accounting()['precision_token_counts']
