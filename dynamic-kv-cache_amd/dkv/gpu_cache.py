@@ -489,12 +489,16 @@ class GPUCache(_CacheBase):
 
         `q_heads` pre-sizes the steps' attention workspace for the launch bounds (so nothing is
         allocated while capturing); graph launches use that buffer, never the one ordinary calls
-        grow. `steps` re-attaches the GraphSteps of an earlier capture on this cache.
+        grow. `steps` re-attaches the GraphSteps of an earlier capture on this cache, or on any
+        cache with the same arena and tile table (a fork of it, or a fork of the cache it forked
+        from): the recorded launches address only those two buffers and the steps' own.
         """
         if len(set(self.seen)) != 1:
             raise ValueError('graph steps need every layer at the same length')
         if steps is not None and steps.cache is not self:
-            raise ValueError('these graph steps belong to another cache')
+            if steps.cache.arena is not self.arena or steps.cache.tiles is not self.tiles:
+                raise ValueError('these graph steps belong to a cache with another arena')
+            steps.cache = self
         self._graph = steps or GraphSteps(self, chunk)
         if q_heads:
             self._graph.workspace(self._graph.workspace_bytes(q_heads))

@@ -58,6 +58,8 @@ class StreamingDecoder:
         self._cache = None  # reused across requests when graphs=True (a captured graph records its buffers)
         self._graphs = {}  # chunk length -> captured forward of that length on self._cache
         self._group_graphs = {}  # (chunk length, k) -> captured forwards of k consecutive chunks (pipelined)
+        self._qa_graphs = {}  # (chunk length, logits, segments) -> captured forward + lm_head on a fork
+        self._qa_seen = set()  # QA shapes already run once eagerly (warms the library paths a capture records)
 
     @property
     def device(self):
@@ -136,7 +138,8 @@ class StreamingDecoder:
     def _reused_cache(self, total):
         if self._cache is None or self._cache.capacity < total:
             self._cache = self.create_cache(max(total, 8192))
-            self._graphs, self._group_graphs = {}, {}  # a captured graph records the old cache's buffers
+            # a captured graph records the old cache's buffers
+            self._graphs, self._group_graphs, self._qa_graphs, self._qa_seen = {}, {}, {}, set()
         else:
             self._cache.reset()
         return self._cache
@@ -250,6 +253,61 @@ class StreamingDecoder:
         self._group_graphs[(chunk, k)] = dict(graph=graph, steps=steps, emb=static_emb, pos=pos, arange=arange,
                                               events=done, streams=streams)
 
+    def _fork_forward(self, branch, ids, logits, lengths=None):
+        """fp32 logits of the last `logits` positions of one forward on a fork of the decoder's
+        reused cache. `lengths` splits the chunk into continuations of the fork's history, each
+        with its own positions and attending to itself only (a block-diagonal chunk mask). With
+        graphs=True a shape seen before replays a captured forward + lm_head (captured the second
+        time it is seen; the first run is eager and warms the library paths)."""
+        emb = self.text.get_input_embeddings()(ids.to(self.device))
+        chunk = emb.shape[1]
+        lengths = list(lengths) if lengths else None
+        segments, rel = None, None
+        if lengths:
+            segments = [0]
+            for n in lengths:
+                segments.append(segments[-1] + n)
+            rel = torch.cat([torch.arange(n, device=self.device) for n in lengths])
+        else:
+            rel = torch.arange(chunk, device=self.device)
+        key = (chunk, int(logits), tuple(lengths) if lengths else None)
+        graphed = self.graphs and self._cache is not None and branch.arena is self._cache.arena
+        if not graphed or key not in self._qa_seen:
+            if graphed:
+                self._qa_seen.add(key)
+            past = branch.get_seq_length()
+            branch.chunk_segments = segments
+            try:
+                return self.forward(branch, embeddings=emb, positions=rel + past, logits=logits)
+            finally:
+                branch.chunk_segments = None
+        fg = self._qa_graphs.get(key)
+        steps = fg['steps'] if fg else None
+        branch.begin_graph_steps(chunk, q_heads=None if fg else self.config.num_attention_heads, steps=steps)
+        try:
+            past = branch.graph_step()
+            if fg is None:
+                static_emb, pos = emb.clone(), torch.empty((1, chunk), dtype=torch.long, device=self.device)
+                torch.add(rel, past, out=pos[0])
+                branch.chunk_segments = segments
+                torch.cuda.synchronize()
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    out = self.text(inputs_embeds=static_emb, past_key_values=branch, use_cache=True,
+                                    position_ids=pos, attention_mask=None, return_dict=True)
+                    lg = self.model.lm_head(out.last_hidden_state[:, -int(logits):]).float()
+                fg = self._qa_graphs[key] = dict(graph=graph, steps=branch._graph, emb=static_emb, pos=pos,
+                                                 rel=rel.clone(), logits=lg)
+                fg['steps'].upload()  # the jobs now carry the K/V addresses recorded in the graph
+            else:
+                fg['emb'].copy_(emb)
+                torch.add(fg['rel'], past, out=fg['pos'][0])
+            fg['graph'].replay()
+            return fg['logits'].clone()
+        finally:
+            branch.chunk_segments = None
+            branch.end_graph_steps()
+
     @staticmethod
     def _mean_loglik(logits, targets):
         return logits.log_softmax(-1).gather(1, targets[:, None]).mean()
@@ -261,7 +319,7 @@ class StreamingDecoder:
         for cand in candidates:
             ids = torch.cat((question_ids, cand), dim=1).to(self.device)
             branch = cache.fork()
-            lg = self.forward(branch, ids=ids, logits=cand.shape[1] + 1)
+            lg = self._fork_forward(branch, ids, cand.shape[1] + 1)
             scores.append(self._mean_loglik(lg[0, :-1], cand[0].to(self.device)))
         return torch.stack(scores)
 
@@ -270,7 +328,7 @@ class StreamingDecoder:
         """The reference's 'label' protocol (src/streaming.py:202-208): one forward of the question
         on a fork; the scores are the last position's logits at the option-label token ids."""
         branch = cache.fork()
-        logits = self.forward(branch, ids=question_ids, logits=1)[0, -1]
+        logits = self._fork_forward(branch, question_ids, 1)[0, -1]
         return logits[torch.as_tensor(label_ids, device=self.device)]
 
     @torch.inference_mode()
@@ -288,18 +346,13 @@ class StreamingDecoder:
     def answer_batched(self, cache, question_ids, candidates):
         """The same scores with the question once and all candidates in one block-diagonal chunk."""
         branch = cache.fork()
-        q_logits = self.forward(branch, ids=question_ids, logits=1)[0]  # predicts each candidate's first token
-        past = branch.get_seq_length()
-        ids = torch.cat(candidates, dim=1).to(self.device)
+        q_logits = self._fork_forward(branch, question_ids, 1)[0]  # predicts each candidate's first token
+        ids = torch.cat(candidates, dim=1)
         bounds = [0]
         for cand in candidates:
             bounds.append(bounds[-1] + cand.shape[1])
-        positions = torch.cat([torch.arange(past, past + c.shape[1], device=self.device) for c in candidates])
-        branch.chunk_segments = bounds
-        try:
-            lg = self.forward(branch, ids=ids, positions=positions, logits=ids.shape[1])[0]
-        finally:
-            branch.chunk_segments = None
+        # every candidate continues the question: positions restart at the fork's length for each
+        lg = self._fork_forward(branch, ids, ids.shape[1], lengths=[c.shape[1] for c in candidates])[0]
         scores = []
         for i, cand in enumerate(candidates):
             pred = torch.cat((q_logits, lg[bounds[i]:bounds[i + 1] - 1]), 0)

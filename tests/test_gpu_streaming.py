@@ -136,6 +136,38 @@ def test_graph_replayed_ingest_matches_eager(cuda, pipeline):
     dec.graphs = False
 
 
+def test_graph_replayed_answers_match_eager(cuda):
+    """With graphs=True the question and candidate forwards on forks of the reused cache replay
+    captured graphs (forward + lm_head) from the third time a shape is seen; every protocol's
+    scores must equal the eager ones bit for bit on each of three requests."""
+    announce('streaming: graph-replayed answers vs eager, three requests')
+    model = build_decoder(**SMALL, seed=31)
+    dec = StreamingDecoder(model, precision='fp32')
+    g = torch.Generator().manual_seed(32)
+    prefix = torch.randint(0, 512, (1, 16), generator=g)
+    question = torch.randint(0, 512, (1, 12), generator=g)
+    cands = [torch.randint(0, 512, (1, n), generator=g) for n in (5, 9, 7)]
+    bits = [4, 8, 16, 4]
+    frames = frames_for(model, len(bits), seed=33)
+
+    def request():
+        cache = dec.ingest(prefix, frames, bits)
+        out = (dec.answer_batched(cache, question, cands), dec.answer(cache, question, cands),
+               dec.answer_labels(cache, question, [3, 5, 7]))
+        torch.cuda.synchronize()
+        return out
+
+    eager = request()
+    dec.graphs = True
+    for i in range(3):
+        got = request()
+        for a, b in zip(got, eager):
+            assert torch.equal(a, b), (i, a, b)
+    # question (shared by the batched and label protocols), candidates batch, three question+candidate
+    assert len(dec._qa_graphs) == 5
+    dec.graphs = False
+
+
 def test_label_protocol_and_calibration_prior(cuda):
     """The 'label' protocol reads the last position's logits at the label ids on a fork (the base
     cache keeps its length), and the calibration prior is the candidate scoring on a prefix-only
