@@ -38,11 +38,20 @@ def parse():
     return p.parse_args()
 
 
+WARM_S = 0.03  # minimum warm-up: after idle the first ~15 ms of launches run ~7% slower (clock ramp)
+
+
 def time_launches(fn, steps, warmup):
+    """ms per fn() over `steps` calls, after `warmup` untimed calls and at least WARM_S seconds of
+    untimed calls (so the timed calls run at the steady-state clock)."""
     import torch
+    t0 = time.perf_counter()
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    while time.perf_counter() - t0 < WARM_S:
+        fn()
+        torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(steps):
