@@ -136,6 +136,40 @@ def test_graph_replayed_ingest_matches_eager(cuda, pipeline):
     dec.graphs = False
 
 
+def test_pipelined_ingest_with_mixed_frame_lengths(cuda):
+    """Groups form only from consecutive frames of one length: with frames of 64, 64, 40, 64, 64,
+    64, 64, 64, 24 tokens and pipeline=3, frames 1-2 and 3-5 replay as groups, 6-7 as a pair,
+    40- and 24-token frames alone. Cache bytes and logits equal the eager ingest's."""
+    announce('streaming: pipelined ingest, mixed frame lengths')
+    model = build_decoder(**SMALL, seed=41)
+    dec = StreamingDecoder(model, precision='fp32', pipeline=3)
+    g = torch.Generator().manual_seed(42)
+    prefix = torch.randint(0, 512, (1, 16), generator=g)
+    question = torch.randint(0, 512, (1, 12), generator=g)
+    lengths = [64, 64, 40, 64, 64, 64, 64, 64, 24]
+    bits = [4, 8, 16, 8, 4, 4, 16, 8, 4]
+    frames = [f[:, :n] for f, n in zip(frames_for(model, len(lengths), seed=43), lengths)]
+
+    def run():
+        cache = dec.ingest(prefix, frames, bits)
+        logits = dec.forward(cache.fork(), ids=question, logits=question.shape[1])
+        torch.cuda.synchronize()
+        return cache, logits
+
+    eager_cache, eager = run()
+    dec.graphs = True
+    for request in range(2):
+        cache, got = run()
+        assert [(s.start, s.rows, s.bits) for s in cache.segments] == \
+            [(s.start, s.rows, s.bits) for s in eager_cache.segments]
+        for layer in (0, SMALL['layers'] - 1):
+            for a, b in zip(cache.materialize(layer), eager_cache.materialize(layer)):
+                assert torch.equal(a, b)
+        assert torch.equal(got, eager), (request, (got - eager).abs().max().item())
+    assert {(64, 3), (64, 2)} <= set(dec._group_graphs)
+    dec.graphs = False
+
+
 def test_graph_replayed_answers_match_eager(cuda):
     """With graphs=True the question and candidate forwards on forks of the reused cache replay
     captured graphs (forward + lm_head) from the third time a shape is seen; every protocol's
