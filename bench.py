@@ -24,7 +24,7 @@ sys.path.insert(0, REPO)
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 LAYERS, HEADS, Q_HEADS, TILE = 32, 5, 15, 64
-PIPELINE = int(os.environ.get('DKV_PIPELINE', '4'))  # frames per pipelined graph replay in the e2e run
+PIPELINE = int(os.environ.get('DKV_PIPELINE', '8'))  # frames per pipelined graph replay in the e2e run
 
 
 def parse():

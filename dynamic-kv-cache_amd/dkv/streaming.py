@@ -45,7 +45,7 @@ def build_decoder(layers=32, hidden=960, heads=15, kv_heads=5, intermediate=2560
 class StreamingDecoder:
     """Frame-by-frame ingestion into a GPUCache and candidate scoring (src/streaming.py:89-237)."""
 
-    def __init__(self, model, fused_ops=True, precision='bf16', graphs=False, pipeline=4):
+    def __init__(self, model, fused_ops=True, precision='bf16', graphs=False, pipeline=8):
         self.model = model
         self.text = model.model
         self.config = model.config
