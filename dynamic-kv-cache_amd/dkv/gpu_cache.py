@@ -622,6 +622,29 @@ class GPUCache(_CacheBase):
         return past, batch
 
 
+def write_job_sources(jobs, kv):
+    """The per-layer fields of a PackJob array (numpy view, GraphSteps.JOB dtype): the K/V views
+    layer l's append recorded (pointer and head/token strides; zeros before the capture) and l."""
+    for l, pair in enumerate(kv):
+        kp, vp, ks, vs = (pair[0].data_ptr(), pair[1].data_ptr(), pair[0].stride(), pair[1].stride()) if pair \
+            else (0, 0, (0, 0, 0, 0), (0, 0, 0, 0))
+        jobs[l] = (kp, vp, ks[1], ks[2], vs[1], vs[2], 0, 0, 0, 0, 0, l, 0, 0, 0)
+
+
+def write_step_jobs(jobs, seg, past, n, write):
+    """The fields every layer's job of one step shares: the segment, the rows being appended and,
+    on layer 0's job only, whether it writes the segment's tile descriptors."""
+    jobs['seg_offset'] = seg.offset
+    jobs['seg_rows'] = seg.rows
+    jobs['seg_token_start'] = seg.start
+    jobs['row0'] = past - seg.start
+    jobs['n'] = n
+    jobs['bits'] = seg.bits
+    jobs['tile_index0'] = seg.tile0
+    jobs['write_tiles'] = 0
+    jobs['write_tiles'][0] = write
+
+
 class GraphSteps:
     """Device-side step parameters of one GPUCache for HIP-graph replays.
 
@@ -699,20 +722,9 @@ class GraphSteps:
             event.synchronize()  # that slot's previous copy has been consumed
         jobs, tail = self.views[self.slot]
         if self.slot_kv[self.slot] != self.kv_version:
-            for l, kv in enumerate(self.kv):
-                kp, vp, ks, vs = (kv[0].data_ptr(), kv[1].data_ptr(), kv[0].stride(), kv[1].stride()) if kv else \
-                    (0, 0, (0, 0, 0, 0), (0, 0, 0, 0))
-                jobs[l] = (kp, vp, ks[1], ks[2], vs[1], vs[2], 0, 0, 0, 0, 0, l, 0, 0, 0)
+            write_job_sources(jobs, self.kv)
             self.slot_kv[self.slot] = self.kv_version
-        jobs['seg_offset'] = seg.offset
-        jobs['seg_rows'] = seg.rows
-        jobs['seg_token_start'] = seg.start
-        jobs['row0'] = past - seg.start
-        jobs['n'] = n
-        jobs['bits'] = seg.bits
-        jobs['tile_index0'] = seg.tile0
-        jobs['write_tiles'] = 0
-        jobs['write_tiles'][0] = write  # layer 0's job writes the segment's tile descriptors
+        write_step_jobs(jobs, seg, past, n, write)
         tail[0], tail[1] = past, c._tiles_before(past)
         if all(kv is not None for kv in self.kv):
             _lib.check(_lib.load().dkv_pack_validate(host.data_ptr(), c.layers, c.arena_bytes, c.layers, c.heads),

@@ -2,7 +2,9 @@
 import pytest
 import torch
 
-from dkv.gpu_cache import GPUCache, segment_bytes, worst_case_arena_bytes
+from dkv import _lib
+from dkv.gpu_cache import GPUCache, GraphSteps, _Segment, segment_bytes, worst_case_arena_bytes, \
+    write_job_sources, write_step_jobs
 
 
 def test_rejects_bad_geometry_and_plans():
@@ -75,3 +77,28 @@ def test_accounting_reference_identities():
     assert a['precision_token_counts'] == {4: 64, 8: 64, 16: 64}
     assert a['gpu_cache_allocated_bytes'] >= a['arena_used_bytes']
     assert a['used_tokens'] == 192 and a['token_mapping_bytes'] == 3 * 16
+
+
+def test_graph_step_jobs_encode_like_ctypes_pack_jobs():
+    """The numpy view a graph step writes into its pinned buffer holds the bytes of the ctypes
+    PackJob array the C ABI reads (the layout, field order and per-layer values)."""
+    import ctypes
+    import numpy as np
+    layers = 3
+    assert GraphSteps.JOB.itemsize == ctypes.sizeof(_lib.PackJob)
+    k = torch.zeros(1, 5, 64, 64, dtype=torch.bfloat16)
+    v = torch.zeros(1, 64, 5, 64, dtype=torch.bfloat16).transpose(1, 2)  # strided V
+    kv = [(k, v), None, (v, k)]
+    buf = np.zeros(layers * GraphSteps.JOB.itemsize, dtype=np.uint8)
+    jobs = buf.view(GraphSteps.JOB)
+    write_job_sources(jobs, kv)
+    for seg, past, n, write in ((_Segment(128, 64, 4, 4096, 2), 128, 64, 1),
+                                (_Segment(100, 101, 8, 1 << 20, 3), 164, 37, 0)):
+        write_step_jobs(jobs, seg, past, n, write)
+        ref = (_lib.PackJob * layers)()
+        for l, pair in enumerate(kv):
+            kp, vp, ks, vs = (pair[0].data_ptr(), pair[1].data_ptr(), pair[0].stride(), pair[1].stride()) if pair \
+                else (0, 0, (0, 0, 0, 0), (0, 0, 0, 0))
+            ref[l] = _lib.PackJob(kp, vp, ks[1], ks[2], vs[1], vs[2], seg.offset, seg.rows, seg.start,
+                                  past - seg.start, n, l, seg.bits, seg.tile0, write if l == 0 else 0)
+        assert buf.tobytes() == bytes(ref)
