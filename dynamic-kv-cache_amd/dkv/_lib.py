@@ -140,7 +140,18 @@ def check(rc, what):
     raise RuntimeError(f'{what}: HIP error {rc}')
 
 
+_raw_stream = getattr(torch._C, '_cuda_getCurrentRawStream', None)
+
+
 def stream_handle(device=None):
+    """torch's current stream on `device` (a torch.device, an index or None: the current device) as
+    a hipStream_t. Every launch asks: the current stream changes under torch.cuda.stream() and
+    during graph capture."""
+    if _raw_stream is not None:
+        if isinstance(device, str):
+            device = torch.device(device)
+        index = device.index if isinstance(device, torch.device) else device
+        return ctypes.c_void_p(_raw_stream(torch.cuda.current_device() if index is None else index))
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
