@@ -17,6 +17,7 @@ gate/up (with post_attention_layernorm) + SiLU*up, down_proj + residual.
 Tensors the kernels do not cover (other dtypes, CPU tensors, other shapes)
 take the reference's own torch composition.
 """
+import functools
 import types
 
 import torch
@@ -98,10 +99,14 @@ def _weight_rows(w):
             and w.stride(0) % 8 == 0 and w.data_ptr() % 16 == 0)
 
 
+@functools.lru_cache(maxsize=None)
+def _linear_supported(rows, n, k, norm, epilogue):
+    return bool(_lib.load().dkv_linear_supported(rows, n, k, norm, epilogue))
+
+
 def linear_covered(rows, weight, norm=False, epilogue=LINEAR_PLAIN):
     """Whether dkv_linear has a launch for x [rows, weight.shape[1]] . weight^T with this prologue/epilogue."""
-    return _weight_rows(weight) and bool(_lib.load().dkv_linear_supported(
-        rows, weight.shape[0], weight.shape[1], int(norm), epilogue))
+    return _weight_rows(weight) and _linear_supported(rows, weight.shape[0], weight.shape[1], int(norm), epilogue)
 
 
 def linear(x, weight, norm=None, eps=1e-6, residual=None, silu_mul=False):
@@ -124,7 +129,7 @@ def linear(x, weight, norm=None, eps=1e-6, residual=None, silu_mul=False):
         r2 = residual.reshape(-1, n_out)
         if r2.shape[0] != rows or r2.stride(-1) != 1 or r2.stride(0) % 4 or r2.data_ptr() % 8:
             return None
-    if not _lib.load().dkv_linear_supported(rows, weight.shape[0], k, int(norm is not None), epi):
+    if not _linear_supported(rows, weight.shape[0], k, int(norm is not None), epi):
         return None
     out = torch.empty((rows, n_out), dtype=x.dtype, device=x.device)
     _lib.check(_lib.load().dkv_linear(
