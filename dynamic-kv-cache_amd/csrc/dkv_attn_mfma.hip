@@ -26,12 +26,15 @@
 //      keys 8g .. 8g+7, the eight k-slots the PV MFMA wants from that group.
 //
 // Splitting the history: with several splits per KV head each workgroup
-// writes unnormalized partials (O, running max, sum) to the workspace and
-// combine_kernel merges them. The partials are stored nontemporally: the end
+// writes partials to the workspace, (running max, sum) per row plus O: fp32
+// and unnormalized at PREC 1 (combine_kernel merges them), fp16 O / sum at
+// PREC 0 (combine_half_kernel; rows past the fp16 range are stored scaled,
+// see half_partial_exponent). The partials are stored nontemporally: the end
 // of a kernel writes every dirty L2 line back, and partials kept out of L2
-// leave nothing to write back (3 us less per launch at past 8128). (Merging in the last-arriving workgroup instead
-// needs a device-scope fence per workgroup, which on gfx950 writes back and
-// invalidates the XCD's L2 and cost far more than the second launch.)
+// leave nothing to write back (3 us less per launch at past 8128). (Merging
+// in the last-arriving workgroup instead needs a device-scope fence per
+// workgroup, which on gfx950 writes back and invalidates the XCD's L2 and
+// cost far more than the second launch.)
 //
 // Precision (template PREC):
 //   0  the reference kernel's rounding points (src/gpu_kernels.py:93-102):
