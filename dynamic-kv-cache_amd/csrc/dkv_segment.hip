@@ -3,7 +3,8 @@
 // (src/kv_quantization.py:12-77), that is a contiguous payload of rows and
 // separate fp32 offset and scale arrays with one group per row.
 //
-// Both directions are byte moves, bound by HBM bandwidth. A wave moves
+// Both directions are byte moves, bound by HBM bandwidth (payload loads are
+// nontemporal: 61-63 -> 55-56 us for the 320 MB pack volume). A wave moves
 // IO_UNITS (layer, kv, head, tile) sub-blocks. Per sub-block that is up to 64
 // payload rows as 16-byte vectors (the rows are contiguous on both sides) and
 // one (offset, scale) pair per lane, split into or joined from the two metadata
@@ -17,9 +18,12 @@ constexpr int IO_THREADS = 256;
 constexpr int IO_WAVES = IO_THREADS / 64;
 constexpr int IO_VECS = TILE * 128 / 16 / 64;  // 16-byte vectors per lane for a full 16-bit sub-block
 #ifndef DKV_IO_UNITS
-#define DKV_IO_UNITS 4
+#define DKV_IO_UNITS 2
 #endif
-constexpr int IO_UNITS = DKV_IO_UNITS;  // sub-blocks per wave, all loaded before any store
+// Sub-blocks per wave, all loaded before any store. With nontemporal loads 2 is
+// best for the pack volume (export / import 53.3 / 53.8 us; 1: 95 us, 3: 55 us,
+// 4: 56 us, 8: 63-64 us).
+constexpr int IO_UNITS = DKV_IO_UNITS;
 
 // Sub-blocks of one segment: one per (layer, kv, head, tile).
 __host__ __device__ inline int io_units(int seg_rows, int n_layers, int heads) {
@@ -82,7 +86,7 @@ __device__ __forceinline__ void io_wave(const dkv_segment_io& s, int w, uint8_t*
 #pragma unroll
     for (int k = 0; k < IO_VECS; ++k) {
       const int i = lane + 64 * k;
-      if (i < nvec) v[q][k] = src[i];
+      if (i < nvec) v[q][k] = __builtin_nontemporal_load(src + i);  // read once: streamed past the caches
     }
     if (bits < 16 && lane < nrows[q]) {
       if (IMPORT)
