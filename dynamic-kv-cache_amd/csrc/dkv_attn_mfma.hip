@@ -145,8 +145,10 @@ __device__ __forceinline__ void raw_load(const dkv_attn_args& a, const Unit& un,
                                            j * a.vn_tok_stride + c * 8);
     }
   } else if (p < (int)(subblock_bytes(un.rows, un.bits) >> 4)) {
-    wk = reinterpret_cast<const uint4*>(un.ksub)[p];
-    wv = reinterpret_cast<const uint4*>(un.vsub)[p];
+    // history bytes are read once per launch: nontemporal loads (past 8128: 19.0 -> 18.6 us per
+    // layer, a decode step 13.6 -> 13.0 us)
+    wk = __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(un.ksub) + p));
+    wv = __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(un.vsub) + p));
   }
 }
 
