@@ -231,6 +231,9 @@ attn_vec_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ part
   }
 }
 
+// Both merges read the partials once, with nontemporal loads (past 8128: 18.7 -> 18.5 us per
+// layer; candidate batches 15.9 -> 15.7 us).
+//
 // Precision-1 merge (unnormalized fp32 O partials, 256 bytes per row): one
 // wave per query row. Lane l = 16 j + c reads 16-byte chunk c (columns
 // 4c + [0, 4)) of split s0 + 4 i + j for i = 0..15, so each load instruction
@@ -260,7 +263,8 @@ combine_kernel(dkv_attn_args a, int splits, const float* __restrict__ part_o,
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int sp = 4 * i + j;
-      raw[i] = sp < cnt ? rows[(base + (int64_t)(s0 + sp) * R) * 16 + c] : make_float4(0.f, 0.f, 0.f, 0.f);
+      const u32x4* src = reinterpret_cast<const u32x4*>(rows) + (base + (int64_t)(s0 + sp) * R) * 16 + c;
+      raw[i] = sp < cnt ? __builtin_bit_cast(float4, __builtin_nontemporal_load(src)) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     float bm = ml.x;
 #pragma unroll
@@ -332,7 +336,8 @@ combine_half_kernel(dkv_attn_args a, int splits, const float* __restrict__ part_
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int s = 8 * i + j;
-      raw[i] = s < cnt ? rows[(base + (int64_t)(s0 + s) * R) * 8 + c] : make_uint4(0, 0, 0, 0);
+      const u32x4* src = reinterpret_cast<const u32x4*>(rows) + (base + (int64_t)(s0 + s) * R) * 8 + c;
+      raw[i] = s < cnt ? __builtin_bit_cast(uint4, __builtin_nontemporal_load(src)) : make_uint4(0, 0, 0, 0);
     }
     float bm = ml.x;
 #pragma unroll
