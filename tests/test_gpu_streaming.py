@@ -93,7 +93,7 @@ def test_mixed_width_ingest_tracks_the_schedule(cuda):
     assert torch.isfinite(logits).all()
 
 
-@pytest.mark.parametrize('pipeline', [1, 2, 3])
+@pytest.mark.parametrize('pipeline', [1, 2, 3, 8])
 def test_graph_replayed_ingest_matches_eager(cuda, pipeline):
     """Frames 2..n replay captured HIP graphs of the decoder forward (launches read their step
     parameters from the device, and the attention runs the splits the host plan would choose for
@@ -120,8 +120,10 @@ def test_graph_replayed_ingest_matches_eager(cuda, pipeline):
     dec.graphs = True
     graph_cache, first = run()
     assert graph_cache is dec._cache
-    # frames 1-5: alone; as pairs 1-2, 3-4 and frame 5 alone; as groups 1-3 and 4-5
-    expect = {1: ({64}, set()), 2: ({64}, {(64, 2)}), 3: (set(), {(64, 3), (64, 2)})}[pipeline]
+    # frames 1-5: alone; as pairs 1-2, 3-4 and frame 5 alone; as groups 1-3 and 4-5; as one group
+    # of 5 (the default depth, 8: more streams than the process's 4 hardware queues)
+    expect = {1: ({64}, set()), 2: ({64}, {(64, 2)}), 3: (set(), {(64, 3), (64, 2)}),
+              8: (set(), {(64, 5)})}[pipeline]
     assert (set(dec._graphs), set(dec._group_graphs)) == expect
     assert graph_cache.plan == eager_cache.plan and graph_cache.seen == eager_cache.seen
     assert [s.frame for s in graph_cache.segments] == [s.frame for s in eager_cache.segments]
