@@ -361,7 +361,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps(dict(error='this build runs on one GPU; --gpus must be 1',
-                              detail='multi-GPU sharding is design-only (DESIGN.md)')), flush=True)
+                              detail='the kernels run one GPU\'s share (a whole layer, or a history '
+                                     'slice via splits); sharding across GPUs is not built')), flush=True)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
