@@ -1,4 +1,5 @@
 """GPUCache bookkeeping on the CPU (device='cpu' arenas; no kernel runs)."""
+import os
 import pytest
 import torch
 
@@ -102,3 +103,16 @@ def test_graph_step_jobs_encode_like_ctypes_pack_jobs():
             ref[l] = _lib.PackJob(kp, vp, ks[1], ks[2], vs[1], vs[2], seg.offset, seg.rows, seg.start,
                                   past - seg.start, n, l, seg.bits, seg.tile0, write if l == 0 else 0)
         assert buf.tobytes() == bytes(ref)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU; --gpus above 1 exits with status 2 and a JSON line that says so."""
+    import json
+    import subprocess
+    import sys
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(repo, 'bench.py'), '--gpus', '2'], cwd=repo,
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 2, r.stderr
+    line = json.loads(r.stdout.strip().splitlines()[-1])
+    assert 'one GPU' in line['error']
