@@ -22,6 +22,10 @@ attention_chunk.npz
   bits [3]      widths of the history tiles (64, 64, 16 tokens)
   out [12, 6, 64] float32: fp64 dequantize-then-SDPA oracle (2 KV heads, 6 Q heads, a 12-token
                 causal chunk after 144 packed history tokens, scale 1/8), rounded to fp32
+  cand_bounds [4], out_cand [12, 6, 64] float32: the same 12 tokens as 3 candidate continuations
+                of 5, 3 and 4 tokens (bounds 0, 5, 8, 12), each causal within itself and blind to
+                the others, all over the full history (the block-diagonal batch of
+                src/streaming.py's candidate scoring)
 """
 import os
 import sys
@@ -97,9 +101,11 @@ def attention_case():
     k = torch.cat(dk + [k_new.float()], 1)
     v = torch.cat(dv + [v_new.float()], 1)
     out = attention(q, k, v, past).float()
+    bounds = [0, 5, 8, 12]
+    out_cand = attention(q, k, v, past, segments=bounds).float()
     return dict(q=bits_u16(q), k_hist=bits_u16(k_hist), v_hist=bits_u16(v_hist), k_new=bits_u16(k_new),
                 v_new=bits_u16(v_new), bits=np.array(bits, np.int32), tiles=np.array(tiles, np.int32),
-                out=out.numpy())
+                out=out.numpy(), cand_bounds=np.array(bounds, np.int32), out_cand=out_cand.numpy())
 
 
 if __name__ == '__main__':

@@ -116,8 +116,9 @@ def test_header_fixture_fields_and_oracle():
         assert np.array_equal(oracle, raw)
 
 
-def numpy_attention(d):
-    """float64 softmax(q k^T / 8 + bottom-right causal mask) v over the dequantized history."""
+def numpy_attention(d, bounds=None):
+    """float64 softmax(q k^T / 8 + bottom-right causal mask) v over the dequantized history; with
+    candidate bounds, chunk token i sees the chunk tokens of its own candidate up to itself."""
     kh, vh = bf16_values(d['k_hist']), bf16_values(d['v_hist'])
     parts_k, parts_v, t0 = [], [], 0
     for b, n in zip(d['bits'], d['tiles']):
@@ -137,10 +138,15 @@ def numpy_attention(d):
     hq, nq, _ = q.shape
     group = hq // k.shape[0]
     out = np.zeros((nq, hq, 64))
+    starts = np.zeros(nq, np.int64)
+    if bounds is not None:
+        for lo, hi in zip(bounds[:-1], bounds[1:]):
+            starts[lo:hi] = lo
     for h in range(hq):
         s = q[h] @ k[h // group].T / 8
         for i in range(nq):
             s[i, past + i + 1:] = -np.inf
+            s[i, past:past + starts[i]] = -np.inf
         p = np.exp(s - s.max(1, keepdims=True))
         out[:, h] = (p / p.sum(1, keepdims=True)) @ v[h // group]
     return out
@@ -150,6 +156,10 @@ def test_attention_fixture_against_numpy():
     d = load('attention_chunk.npz')
     ref = numpy_attention(d)
     assert np.abs(ref - d['out']).max() <= 1e-5 * max(1.0, np.abs(ref).max())
+    cand = numpy_attention(d, d['cand_bounds'].tolist())
+    assert np.abs(cand - d['out_cand']).max() <= 1e-5 * max(1.0, np.abs(cand).max())
+    # the first candidate's rows see exactly what the plain chunk's first rows see
+    assert np.array_equal(d['out_cand'][:5], d['out'][:5])
 
 
 def test_oracle_reproduces_attention_fixture():
@@ -164,3 +174,5 @@ def test_oracle_reproduces_attention_fixture():
     v = torch.cat(dv + [bf16_tensor(d['v_new']).float()], 1)
     out = attention(bf16_tensor(d['q']), k, v, t0).float().numpy()
     assert np.abs(out - d['out']).max() <= 1e-6
+    cand = attention(bf16_tensor(d['q']), k, v, t0, segments=d['cand_bounds'].tolist()).float().numpy()
+    assert np.abs(cand - d['out_cand']).max() <= 1e-6

@@ -3,7 +3,8 @@
 pack_rows.npz: the 64 rows appended as one K/V segment of one head must give the fixture's
 payload, offsets and scales bit for bit at 4, 8 and 16 bits, and the segment's export must carry
 the fixture's PackedTensor header and bytes. attention_chunk.npz: the history appended tile by
-tile at the fixture's widths, then the 12-token chunk attended with precision='fp32', must be
+tile at the fixture's widths, then the 12-token chunk (and the same tokens as 3 candidates of 5, 3 and
+4 tokens, a block-diagonal batch) attended with precision='fp32', must be
 within 1e-3 (max-abs) of the stored fp64 oracle output; with precision='bf16' (the reference
 kernel's bf16 rounding of K, V and p) within the reference's own scenario tolerance,
 atol 0.035 + rtol 0.015 (tests/test_gpu_backend.py:82-101).
@@ -58,9 +59,10 @@ def test_pack_matches_golden_bytes(cuda, bits):
         assert np.array_equal(key.scales.cpu().numpy().view(np.uint32), d[f'scale{bits}'])
 
 
+@pytest.mark.parametrize('candidates', [False, True])
 @pytest.mark.parametrize('precision', ['fp32', 'bf16'])
-def test_attention_matches_golden_output(cuda, precision):
-    announce(f'golden attention chunk precision={precision}')
+def test_attention_matches_golden_output(cuda, precision, candidates):
+    announce(f'golden attention chunk precision={precision} candidates={candidates}')
     d = load('attention_chunk.npz')
     k_hist, v_hist = bf16_tensor(d['k_hist']), bf16_tensor(d['v_hist'])
     H, past = k_hist.shape[:2]
@@ -75,8 +77,10 @@ def test_attention_matches_golden_output(cuda, precision):
     c.select(16)
     p = c.append(kn, vn, 0)
     assert p == past
-    out = c.attend(q, kn, vn, 0, p, out_dtype=torch.float32, precision=precision)[0].cpu().double()
-    ref = torch.from_numpy(d['out']).double()
+    segments = d['cand_bounds'].tolist() if candidates else None
+    out = c.attend(q, kn, vn, 0, p, out_dtype=torch.float32, segments=segments,
+                   precision=precision)[0].cpu().double()
+    ref = torch.from_numpy(d['out_cand' if candidates else 'out']).double()
     err = (out - ref).abs()
     if precision == 'fp32':
         assert err.max().item() <= 1e-3, err.max().item()
