@@ -258,7 +258,7 @@ def bench_candidates(bits, steps, warmup, rotate, precision='bf16'):
 
 
 def bench_e2e(frame_counts=(16, 64, 96), reps=2):
-    """random-init 32-layer decoder, 64-token synthetic frames, 4 candidates.
+    """Streaming request: random-init 32-layer decoder, 64-token synthetic frames, 4 candidates.
 
     frames/s = frames / (ingest + candidate scoring) seconds, the reference's request definition
     (benchmarks/gpu_evaluate.py:105) without video decode and the vision encoder.
