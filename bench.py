@@ -360,7 +360,7 @@ def cpu_baselines(target_s=8.0):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps(dict(error='this build runs on one GPU; --gpus must be 1',
+        print(json.dumps(dict(error='bench.py measures one GPU; --gpus must be 1',
                               detail='the kernels run one GPU\'s share (a whole layer, or a history '
                                      'slice via splits); sharding across GPUs is not built')), flush=True)
         sys.exit(2)

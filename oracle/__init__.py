@@ -1,8 +1,8 @@
 """CPU oracle for the packed mixed-precision KV path. TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
-this package, and only as the checker (or, for the baseline, as the timed CPU
-restatement of the reference's CPU path). The product path (the dkv package and
+this package, and only as the expected result a test compares against (or, for the
+baseline, as the timed CPU restatement of the reference's CPU path). The product path (the dkv package and
 libdkv.so) never imports it and has no CPU fallback.
 
 Modules:

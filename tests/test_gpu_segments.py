@@ -2,7 +2,7 @@
 PackedTensor + segment-descriptor layout (src/kv_quantization.py:12-77,
 src/cache_manager.py:9-58).
 
-The checker is the oracle's restatement of the reference CPU cache
+The expected bytes come from the oracle's restatement of the reference CPU cache
 (oracle/cpu_path.py MixedPrecisionCache). Fed the same K/V, select() calls and
 layer order as a GPUCache, its segments must equal GPUCache.export_segments()
 byte for byte: payload, fp32 offsets and scales (compared as bit patterns),
