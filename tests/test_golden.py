@@ -176,3 +176,20 @@ def test_oracle_reproduces_attention_fixture():
     assert np.abs(out - d['out']).max() <= 1e-6
     cand = attention(bf16_tensor(d['q']), k, v, t0, segments=d['cand_bounds'].tolist()).float().numpy()
     assert np.abs(cand - d['out_cand']).max() <= 1e-6
+
+
+def test_committed_script_regenerates_the_fixtures():
+    """tests/golden/make_golden.py, run again, gives the committed arrays (pack bit for bit; the
+    fp64 attention outputs, stored as fp32, within 1e-6 across BLAS builds)."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location('make_golden', os.path.join(GOLDEN, 'make_golden.py'))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    for name, fresh in (('pack_rows.npz', mod.pack_rows_case()), ('attention_chunk.npz', mod.attention_case())):
+        stored = load(name)
+        assert sorted(stored.files) == sorted(fresh), name
+        for key, value in fresh.items():
+            if value.dtype.kind == 'f':
+                assert np.abs(value - stored[key]).max() <= 1e-6, (name, key)
+            else:
+                assert np.array_equal(value, stored[key]), (name, key)
