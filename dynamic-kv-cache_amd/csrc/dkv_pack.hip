@@ -67,6 +67,12 @@ __device__ __forceinline__ RowDst row_dst(const dkv_pack_job& j, int kv, int hea
   return d;
 }
 
+// The offset of a row whose minimum is zero: -0 when the row holds a -0, else
+// +0, the sign IEEE 754-2019 minimum() gives. (v_min_f32 and torch's amin,
+// src/kv_quantization.py:63, leave it to the order of the reduction; codes,
+// scales and dequantized values do not depend on it.)
+__device__ __forceinline__ float zero_min_sign(uint32_t has_neg_zero) { return has_neg_zero ? -0.0f : 0.0f; }
+
 // Codes of 8 elements of a row whose (offset, scale) is (a, s), with r ~ 1/s,
 // packed: BITS 4 -> out[0] (element e in bits 4e..4e+3), BITS 8 -> out[0..1]
 // (element e in byte e). `fast` says r and every t below are finite.
@@ -166,6 +172,12 @@ __device__ __forceinline__ void pack_loaded(const dkv_pack_job& j, int kv, int h
   for (int e = 1; e < 64; ++e) {
     lo = fminf(lo, x[e]);
     hi = fmaxf(hi, x[e]);
+  }
+  if (lo == 0.0f) {  // rare: the sign of a zero minimum (see zero_min_sign)
+    uint32_t nz = 0;
+#pragma unroll
+    for (int e = 0; e < 64; ++e) nz |= __float_as_uint(x[e]) == 0x80000000u;
+    lo = zero_min_sign(nz);
   }
   const float a = lo;
   const float span = hi - a;
@@ -311,12 +323,16 @@ __device__ __forceinline__ void pack_row8(const dkv_pack_job& j, int kv, int hea
     lo = fminf(lo, x[e]);
     hi = fmaxf(hi, x[e]);
   }
+  uint32_t nz = 0;  // the row holds a -0 (the sign of a zero minimum, see zero_min_sign)
+#pragma unroll
+  for (int e = 0; e < 8; ++e) nz |= __float_as_uint(x[e]) == 0x80000000u;
 #pragma unroll
   for (int o = 1; o < 8; o <<= 1) {
     lo = fminf(lo, __shfl_xor(lo, o));
     hi = fmaxf(hi, __shfl_xor(hi, o));
+    nz |= __shfl_xor(nz, o);
   }
-  const float a = lo;
+  const float a = lo == 0.0f ? zero_min_sign(nz) : lo;
   const float span = hi - a;
   const float s = span > 0.0f ? __fdiv_rn(span, BITS == 4 ? 15.0f : 255.0f) : 1.0f;
   const float rs = __builtin_amdgcn_rcpf(s);

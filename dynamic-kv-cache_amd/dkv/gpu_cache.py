@@ -32,6 +32,16 @@ PRECISIONS = {'bf16': 0, 'fp32': 1}
 PATHS = {'auto': 0, 'vector': 1, 'mfma': 2}
 
 
+# The kernels store bf16 or fp32 (dkv_attn_args.out_dtype, dkv_reconstruct's out_dtype); any other
+# dtype would receive bf16 bit patterns.
+OUT_DTYPES = (torch.bfloat16, torch.float32)
+
+
+def _check_dtype(dtype, what):
+    if dtype not in OUT_DTYPES:
+        raise ValueError(f'{what} must be torch.bfloat16 or torch.float32, got {dtype}')
+
+
 def row_bytes(bits):
     return {4: 32, 8: 64, 16: 128}[bits]
 
@@ -85,6 +95,7 @@ class GPUCache(_CacheBase):
             raise ValueError('GPU kernel currently supports head_dim=64')
         if precision not in PRECISIONS:
             raise ValueError(f'precision must be one of {sorted(PRECISIONS)}')
+        _check_dtype(dtype, 'dtype')
         self.precision = precision
         self.layers, self.heads, self.dim = layers, heads, dim
         self.dtype, self.device = dtype, torch.device(device)
@@ -123,9 +134,14 @@ class GPUCache(_CacheBase):
                 self._open_segment(self.segments[-1].end if self.segments else 0, n, bits)
 
     # -- bookkeeping -------------------------------------------------------
-    def _open_segment(self, start, n, bits, frame=-1):
+    def _open_segment(self, start, n, bits, frame=-1, grow=True):
         need = segment_bytes(n, bits, self.layers, self.heads)
         if self.arena_used + need > self.arena_bytes:
+            if not grow:
+                # a captured graph recorded the arena's address: a new arena would leave its
+                # launches writing freed memory
+                raise ValueError(f'graph steps cannot grow the arena: a {n}-token {bits}-bit segment needs '
+                                 f'{self.arena_used + need} bytes, the arena holds {self.arena_bytes}')
             self._grow(self.arena_used + need)
         tile0 = len(self.tile_starts)
         if tile0 + (n + TILE - 1) // TILE > self.tiles.shape[0]:
@@ -359,7 +375,7 @@ class GPUCache(_CacheBase):
         a.n_tiles, a.past = self._tiles_before(past), past
         a.layer, a.layers, a.heads, a.q_heads, a.nq = layer, self.layers, self.heads, q.shape[1], nq
         if segments:
-            if len(segments) + 1 > _lib.DKV_MAX_CHUNK_SEGS + 1:
+            if len(segments) - 1 > _lib.DKV_MAX_CHUNK_SEGS:  # bounds [0, b1, ..., nq]: one more than segments
                 raise ValueError(f'at most {_lib.DKV_MAX_CHUNK_SEGS} chunk segments')
             a.n_segs = len(segments) - 1
             for i, b in enumerate(segments):
@@ -374,8 +390,7 @@ class GPUCache(_CacheBase):
         return a
 
     def _workspace_for(self, nbytes):
-        # Zero-filled once: the attention kernels keep their arrival counters in it and leave
-        # them zero after every call.
+        # Split partials of the attention kernels: every call writes what its merge reads.
         if self._workspace is None or self._workspace.numel() < nbytes or self._workspace.device != self.device:
             self._workspace = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=self.device)
         return self._workspace
@@ -405,8 +420,10 @@ class GPUCache(_CacheBase):
             segments = self.chunk_segments
         if segments is not None and (segments[0] != 0 or segments[-1] != n):
             raise ValueError(f'chunk segments {segments} do not cover the {n}-token chunk')
+        out_dtype = out_dtype or q.dtype
+        _check_dtype(out_dtype, 'attend output dtype')
         q, k, v = self._kv_view(q), self._kv_view(k), self._kv_view(v)
-        out = torch.empty((1, n, q.shape[1], self.dim), dtype=out_dtype or q.dtype, device=q.device)
+        out = torch.empty((1, n, q.shape[1], self.dim), dtype=out_dtype, device=q.device)
         if self._graph is not None:
             a = self._graph.attend_args(q, k, v, layer, out, segments, path, splits, precision)
         else:
@@ -425,7 +442,9 @@ class GPUCache(_CacheBase):
     def materialize(self, layer, out_dtype=None):
         """Dequantized history of one layer: (k, v), each [1, H, seen, 64] (src/gpu_cache.py:106-112)."""
         n = self.seen[layer]
-        out = torch.empty((2, self.heads, n, self.dim), dtype=out_dtype or self.dtype, device=self.device)
+        out_dtype = out_dtype or self.dtype
+        _check_dtype(out_dtype, 'materialize output dtype')
+        out = torch.empty((2, self.heads, n, self.dim), dtype=out_dtype, device=self.device)
         if n:
             lib = _lib.load()
             _lib.check(lib.dkv_reconstruct(self.arena.data_ptr(), self.tiles.data_ptr(), self._tiles_before(n), n,
@@ -496,7 +515,7 @@ class GPUCache(_CacheBase):
         if len(set(self.seen)) != 1:
             raise ValueError('graph steps need every layer at the same length')
         if steps is not None and steps.cache is not self:
-            if steps.cache.arena is not self.arena or steps.cache.tiles is not self.tiles:
+            if steps.arena is not self.arena or steps.tiles is not self.tiles:
                 raise ValueError('these graph steps belong to a cache with another arena')
             steps.cache = self
         self._graph = steps or GraphSteps(self, chunk)
@@ -660,14 +679,15 @@ class GraphSteps:
 
     def __init__(self, cache, chunk):
         self.cache, self.chunk = cache, chunk
+        # the buffers the recorded launches address: step() refuses to run once the cache holds others
+        self.arena, self.tiles = cache.arena, cache.tiles
         self.job_bytes = ctypes.sizeof(_lib.PackJob)
         self.nbytes = cache.layers * self.job_bytes + 8
         with torch.inference_mode(False):  # ordinary tensors: step() may run inside or outside inference mode
             self.dev = torch.zeros(self.nbytes, dtype=torch.uint8, device=cache.device)
-            self.ring = [(torch.zeros(self.nbytes, dtype=torch.uint8, pin_memory=True), None)
-                         for _ in range(self.RING)]
+        self.ring = None  # pinned host copies, allocated by the first upload()
+        self.views = None
         self.slot = 0
-        self.views = [self._view(host) for host, _ in self.ring]
         self.kv = [None] * cache.layers  # (k, v) views append() recorded, kept alive with the graph
         self.kv_version = 0  # bumped whenever append() records a view
         self.slot_kv = [-1] * self.RING  # kv_version each slot's pointer fields were written with
@@ -683,15 +703,22 @@ class GraphSteps:
                 self.ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=self.cache.device)
         return self.ws
 
+    def _check_storage(self):
+        c = self.cache
+        if c.arena is not self.arena or c.tiles is not self.tiles:
+            raise ValueError('the cache no longer holds the arena and tile table these graph steps recorded '
+                             '(it grew or was rebuilt): capture again')
+
     def step(self):
         c, n = self.cache, self.chunk
+        self._check_storage()
         past = c.seen[0]
         if len(set(c.seen)) != 1:
             raise ValueError('graph steps need every layer at the same length')
         if past + n > c.capacity:
             raise ValueError('GPU context limit exceeded')
         if c.online:
-            seg = c._open_segment(past, n, c.pending_bits, c.frame_id)
+            seg = c._open_segment(past, n, c.pending_bits, c.frame_id, grow=False)
             write = 1
         else:
             seg = next((s for s in c.segments if s.start <= past < s.end), None)
@@ -716,7 +743,13 @@ class GraphSteps:
     def upload(self):
         """Writes the current step's jobs and bounds to the device buffer (async, stream-ordered)."""
         c, n = self.cache, self.chunk
+        self._check_storage()
         past, seg, write = self.state
+        if self.ring is None:
+            with torch.inference_mode(False):
+                self.ring = [(torch.zeros(self.nbytes, dtype=torch.uint8, pin_memory=True), None)
+                             for _ in range(self.RING)]
+            self.views = [self._view(host) for host, _ in self.ring]
         host, event = self.ring[self.slot]
         if event is not None:
             event.synchronize()  # that slot's previous copy has been consumed

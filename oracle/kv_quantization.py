@@ -5,7 +5,8 @@ pack(tensor, bits, group_size=64) follows src/kv_quantization.py:41-77:
     finite values (:42-48), else ValueError;
   - 16-bit: fp16/bf16 bytes kept verbatim, other floats cast to fp16 (:49-55);
   - 4/8-bit: flatten, groups of `group_size` padded by repeating the last value
-    (:57-62); offset = group min (:63); span = max - offset (:64);
+    (:57-62); offset = group min (:63; a zero minimum carries the IEEE 754-2019
+    minimum()'s sign, see canonical_zero_min); span = max - offset (:64);
     scale = span / (2^b - 1) if span > 0 else 1 (:65);
     q = round_half_even((x - offset) / scale) clamped to [0, 2^b - 1] (:66-67);
     4-bit payload byte i = q[2i] | q[2i+1] << 4 (:68-71);
@@ -55,13 +56,27 @@ class PackedTensor:
         return self.payload_bytes + self.metadata_bytes
 
 
+def canonical_zero_min(groups, offsets):
+    """The sign of a zero group minimum, fixed as IEEE 754-2019 minimum() fixes it: -0 when the
+    group holds a -0 (and no negative value), else +0.
+
+    The reference's offset is torch's amin (src/kv_quantization.py:63), whose sign for a minimum
+    that is a zero present with both signs depends on the reduction order of the build and CPU it
+    runs on. Codes, scales and dequantized values do not depend on that sign; this pins the one
+    bit left open so that packed bytes compare bit for bit.
+    """
+    neg_zero = (groups.view(torch.int32) == -0x80000000).any(dim=1)
+    zero = offsets == 0
+    return torch.where(zero, torch.where(neg_zero, -0.0, 0.0), offsets)
+
+
 def quantize_groups(groups, bits):
     """Per-group affine codes of a float32 [n_groups, group_size] tensor.
 
     Returns (codes uint8, offsets fp32, scales fp32) with the reference's op order.
     """
     levels = (1 << bits) - 1
-    offsets = groups.amin(dim=1)
+    offsets = canonical_zero_min(groups, groups.amin(dim=1))
     spans = groups.amax(dim=1) - offsets
     scales = torch.where(spans > 0, spans / levels, torch.ones_like(spans))
     q = ((groups - offsets[:, None]) / scales[:, None]).round().clamp(0, levels)

@@ -11,7 +11,8 @@ a numpy restatement. The GPU tests compare libdkv with the stored bytes and valu
 pack_rows.npz
   x            [64, 64] uint16   bf16 bits of the source rows: half-way ties at 4 and 8 bits,
                                  a constant row, wide / tiny / subnormal / near-fp32-max spans,
-                                 one-sided rows, then seeded N(0, 1) rows with 4 outlier
+                                 one-sided rows, zero minima with both signs (offset -0) and
+                                 with +0 only, then seeded N(0, 1) rows with 4 outlier
                                  channels x 8 (the metric's value generator)
   payload{b}   [64, row bytes]   uint8 codes of src/kv_quantization.py:pack at b = 4, 8, 16
   offset{b}, scale{b} [64]       uint32 fp32 bits (b = 4, 8)
@@ -65,8 +66,12 @@ def pack_rows_case():
     rows[8] = 0.25
     rows[8, 17] = 96.0  # one outlier above a constant floor
     rows[9] = torch.arange(64, dtype=torch.float32) % 3 - 1  # three levels
+    rows[10] = torch.arange(64, dtype=torch.float32) / 8
+    rows[10, 0], rows[10, 37] = 0.0, -0.0  # zero minimum with both signs: offset -0
+    rows[11] = torch.arange(64, dtype=torch.float32) % 5
+    rows[11, 50] = 0.0  # zero minimum, only +0: offset +0
     g = torch.Generator().manual_seed(20240611)
-    rows[10:] = outlier_rows((54, 64), g).float()
+    rows[12:] = outlier_rows((52, 64), g).float()
     x = rows.to(torch.bfloat16)
     out = {'x': bits_u16(x)}
     for b in (4, 8, 16):

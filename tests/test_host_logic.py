@@ -116,3 +116,50 @@ def test_bench_refuses_more_than_one_gpu():
     assert r.returncode == 2, r.stderr
     line = json.loads(r.stdout.strip().splitlines()[-1])
     assert 'one GPU' in line['error']
+
+
+def test_graph_steps_refuse_to_grow_the_arena():
+    """A captured graph recorded the arena's address: a step whose segment does not fit the arena
+    raises instead of growing it (a grown arena would leave the recorded launches on freed memory),
+    and steps refuse to run once the cache holds another arena."""
+    c = GPUCache(None, layers=2, heads=5, max_tokens=4096, arena_bytes=1 << 16, device='cpu')
+    steps = c.begin_graph_steps(64)
+    c.select(16)
+    arena = c.arena
+    with pytest.raises(ValueError, match='cannot grow the arena'):
+        steps.step()
+    assert c.arena is arena and c.arena_bytes == 1 << 16 and c.segments == []
+    c.end_graph_steps()
+    c.reserve(16, 2048)  # an ordinary reserve() may grow it
+    assert c.arena is not arena
+    with pytest.raises(ValueError, match='no longer holds'):
+        c.begin_graph_steps(64, steps=steps)
+        steps.step()
+
+
+def test_unsupported_dtypes_are_rejected():
+    """The kernels store bf16 or fp32 only: fp16 caches and outputs raise instead of receiving
+    bf16 bit patterns."""
+    with pytest.raises(ValueError, match='dtype'):
+        GPUCache(None, layers=1, device='cpu', dtype=torch.float16)
+    c = GPUCache(None, layers=1, heads=1, max_tokens=64, device='cpu', dtype=torch.float32)
+    with pytest.raises(ValueError, match='dtype'):
+        c.materialize(0, out_dtype=torch.float16)
+
+
+@pytest.mark.parametrize('n_segs,ok', [(16, True), (17, False)])
+def test_chunk_segment_limit(n_segs, ok):
+    """attend_args accepts exactly DKV_MAX_CHUNK_SEGS segments (17 bounds) and rejects one more."""
+    c = GPUCache(None, layers=1, heads=1, max_tokens=128, device='cpu')
+    nq = 32
+    q = torch.zeros(1, 3, nq, 64, dtype=torch.bfloat16)
+    kv = torch.zeros(1, 1, nq, 64, dtype=torch.bfloat16)
+    out = torch.zeros(1, nq, 3, 64, dtype=torch.bfloat16)
+    bounds = list(range(0, 2 * n_segs, 2))[:n_segs] + [nq]
+    assert len(bounds) == n_segs + 1
+    if ok:
+        a = c.attend_args(q, kv, kv, 0, 0, out, bounds)
+        assert a.n_segs == n_segs and list(a.seg_bounds)[:n_segs + 1] == bounds
+    else:
+        with pytest.raises(ValueError, match='at most 16'):
+            c.attend_args(q, kv, kv, 0, 0, out, bounds)

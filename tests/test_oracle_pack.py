@@ -56,12 +56,20 @@ def test_reject_bad_arguments():
         pack(torch.zeros(1, 1, 0, 64), 8)
 
 
+def ieee_min(x):
+    """Row minima of float32 rows as IEEE 754-2019 minimum() defines them: a zero minimum is -0 when
+    the row holds a -0 (numpy's min leaves that sign to the order of the reduction)."""
+    a = x.min(1)
+    neg_zero = (x.view(np.uint32) == 0x80000000).any(1)
+    return np.where(a == 0, np.where(neg_zero, np.float32(-0.0), np.float32(0.0)), a).astype(np.float32)
+
+
 # -- independent restatement: numpy float32 ----------------------------------------------------
 def numpy_pack_rows(x, bits):
     """Row-wise affine codes computed with numpy's IEEE float32 ops (not torch)."""
     x = np.asarray(x, dtype=np.float32)
     levels = np.float32((1 << bits) - 1)
-    a = x.min(axis=1)
+    a = ieee_min(x)
     span = (x.max(axis=1) - a).astype(np.float32)
     s = np.where(span > 0, span / levels, np.float32(1)).astype(np.float32)
     q = np.clip(np.rint((x - a[:, None]) / s[:, None]), 0, levels).astype(np.uint8)
@@ -131,3 +139,28 @@ def test_header_bytes_literal():
     p16 = pack(torch.zeros(1, 2, 3, 64, dtype=torch.bfloat16), 16)
     assert bytes(p16.header.tolist())[:8] == b'DKVC' + bytes([1, 16, 2, 4])
     assert p16.fields() == (16, 2, (1, 2, 3, 64), 64, 384, 0)
+
+
+@pytest.mark.parametrize('bits', [4, 8])
+def test_zero_minimum_takes_the_ieee_minimum_sign(bits):
+    """A row whose minimum is zero gets offset -0 when it holds a -0 and +0 otherwise, wherever
+    the zeros sit (torch's amin leaves that sign to its reduction order); codes and scales do not
+    depend on it."""
+    g = torch.Generator().manual_seed(7)
+    base = torch.rand(6, 64, generator=g) + 0.5
+    rows = base.clone()
+    rows[0, 3], rows[0, 40] = 0.0, -0.0  # both signs, +0 first
+    rows[1, 3], rows[1, 40] = -0.0, 0.0  # both signs, -0 first
+    rows[2, 63] = -0.0                   # only -0
+    rows[3, 0] = 0.0                     # only +0
+    rows[4, :] = -0.0                    # constant -0: scale 1
+    rows[5, 10], rows[5, 11] = -0.0, -1.0  # negative minimum: the zero's sign is irrelevant
+    x = rows.bfloat16()
+    payload, off, sc = pack_rows(x, bits)
+    bits_of = off.view(torch.int32).tolist()
+    assert bits_of[:5] == [-0x80000000, -0x80000000, -0x80000000, 0, -0x80000000]
+    assert off[5].item() == -1.0
+    plus = x.float().abs().where(x.float() == 0, x.float()).bfloat16()  # every -0 made +0
+    p2, o2, s2 = pack_rows(plus, bits)
+    assert torch.equal(payload, p2) and torch.equal(sc, s2)
+    assert o2.view(torch.int32)[:5].tolist() == [0, 0, 0, 0, 0]
