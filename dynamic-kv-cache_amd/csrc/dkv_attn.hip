@@ -193,12 +193,15 @@ attn_vec_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ part
     }
   }
 
-  // Epilogue: final output (one split) or partials.
+  // Epilogue: final output (one split running) or partials. The test is on the
+  // splits that run, not the launch's: a graph replay over a short history can
+  // run one split of a launch sized for more, and must then store exactly what
+  // a direct one-split call stores (the merge kernels skip such launches).
 #pragma unroll
   for (int i = 0; i < VEC_RPW; ++i) {
     const int r = rg * VEC_ROWS + w * VEC_RPW + i;
     if (r >= R) break;
-    if (splits == 1) {
+    if (active == 1) {
       const int g = r / a.nq, m = r - g * a.nq;
       const float o = acc[i] / sm[i];
       const int64_t off = (int64_t)m * a.out_tok_stride + (int64_t)(h * G + g) * a.out_head_stride + lane;
@@ -252,6 +255,7 @@ combine_kernel(dkv_attn_args a, int splits, const float* __restrict__ part_o,
   int units = 0;
   Hist hs;
   const int active = runtime_plan(a, hs, units, splits);  // partials written (graph replays: fewer)
+  if (active <= 1) return;  // one split ran and stored the output itself
   const int64_t base = (int64_t)h * splits * R + r;
   const int j = lane >> 4, c = lane & 15;
   const float4* rows = reinterpret_cast<const float4*>(part_o);  // 16 chunks of 16 bytes per row
@@ -323,6 +327,7 @@ combine_half_kernel(dkv_attn_args a, int splits, const float* __restrict__ part_
   int units = 0;
   Hist hs;
   const int active = runtime_plan(a, hs, units, splits);  // partials written (graph replays: fewer)
+  if (active <= 1) return;  // one split ran and stored the output itself
   const int64_t base = (int64_t)h * splits * R + r;
   const int j = lane >> 3, c = lane & 7;
   const uint4* rows = reinterpret_cast<const uint4*>(part_o);  // 8 chunks of 16 bytes per row

@@ -502,7 +502,7 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ par
       for (int db = 0; db < 4; ++db)
         o[db] = acc_o[nb][db] * f0 + *reinterpret_cast<const f32x4*>(mrg_o + lr * MRG_STRIDE + 16 * db + 4 * g) * f1;
       if (r >= R) continue;
-      if (splits == 1) {
+      if (active == 1) {  // the splits that run (see attn_vec_kernel's epilogue)
         const int gq = r / a.nq, m = r - gq * a.nq;
         const float inv = 1.f / l;
         const int64_t off = (int64_t)m * a.out_tok_stride + (int64_t)(h * G + gq) * a.out_head_stride + 4 * g;

@@ -5,17 +5,16 @@ Tolerances:
   precision='fp32', bf16 output vs the same oracle: |out - oracle| <= 1e-3 + 2^-8 |oracle| (the
     bf16 store rounds to nearest, at most half an ulp = 2^-8 relative).
   precision='bf16' (the reference kernel's rounding of K, V and p to bf16) vs the emulated
-    reference kernel (oracle.attention.reference_semantics):
-    - one split (the reference's own key order, so p is rounded against the same running max):
-      fp32 output max-abs <= 2e-2 on the metric's frame-chunk and candidate workloads. The MFMA
-      kernel's two key groups keep running maxima over 32 keys of each unit, so the seeded
-      random-shape sweep bounds one split like the default split below;
-    - the default split history: each split rounds p against its own running max, so the result
-      also carries the reference's own dependence on where its 64-key blocks fall. The bound is
-      2e-2 plus that dependence measured on the same input (reference at 32-key blocks vs 64-key
-      blocks), which is up to 1.5e-2 on the outlier-channel data;
-    - bf16 output: the fp32 bound + 2^-7 |ref|, since two bf16 roundings of nearby values can land
+    reference kernel (oracle.attention.reference_semantics), on the metric's frame-chunk and
+    candidate workloads, at one split and at the default split count (the path bench.py times):
+    - fp32 output max-abs <= max(2e-2, noise), where noise is the reference's own distance from
+      the same computation with p unrounded on that input (reference_noise). Each split rounds p
+      against its own running max, the reference against its running max over 64-key blocks, so
+      two correct implementations differ by about that noise: on the outlier-channel data it is
+      1.3e-2 to 1.8e-2, and 2.2e-2 at past 1024. The tests print the measured max-abs and noise;
+    - bf16 output: the same bound + 2^-7 |ref|, since two bf16 roundings of nearby values can land
       one bf16 ulp (2^-7 relative) apart and outlier-channel outputs reach |O| ~ 20 (ulp 0.125).
+    The seeded random-shape sweep and the 128-split merge test use the same bound.
   The reference's own scenarios keep their tolerances (atol .035, rtol .015; max-abs < .035).
 """
 import pytest
@@ -75,32 +74,44 @@ def semantics_out(case, dk, dv, segments=None, out_dtype=torch.bfloat16):
     return reference_semantics(case['q'], k, v, dk.shape[1], segments=segments, out_dtype=out_dtype).double()
 
 
-def block_sensitivity(case, dk, dv, segments=None):
-    """max |reference(32-key blocks) - reference(64-key blocks)| on this input."""
+def reference_noise(case, dk, dv, segments=None):
+    """max |reference kernel - the same computation with p unrounded| on this input: the reference's
+    own bf16 rounding error of p (K and V rounded to bf16 in both). An implementation that rounds p
+    against other running maxima (any split of the history) differs from the reference by about
+    this much even when it is exact, so the bound is max(2e-2, this)."""
     k = torch.cat((dk, case['k_new'].float()), 1)
     v = torch.cat((dv, case['v_new'].float()), 1)
-    b32 = reference_semantics(case['q'], k, v, dk.shape[1], block=32, segments=segments, out_dtype=torch.float32)
-    b64 = reference_semantics(case['q'], k, v, dk.shape[1], block=64, segments=segments, out_dtype=torch.float32)
-    return (b32 - b64).abs().max().item()
+    ref = reference_semantics(case['q'], k, v, dk.shape[1], segments=segments, out_dtype=torch.float32).double()
+    exact_p = attention(case['q'], k.to(torch.bfloat16).float(), v.to(torch.bfloat16).float(), dk.shape[1],
+                        segments=segments)
+    return (ref - exact_p).abs().max().item()
 
 
-def assert_semantics(c, case, dk, dv, cuda, path, segments=None):
+def assert_semantics(c, case, dk, dv, cuda, path, segments=None, label=''):
+    """bf16 precision against the emulated reference kernel, at one split and at the default split
+    count (the path bench.py times): fp32 output max-abs <= max(2e-2, the reference's own p-rounding
+    noise on this input), and bf16 output within that plus one bf16 ulp of the reference's bf16
+    output. Prints the measured errors and the noise."""
     ref32 = semantics_out(case, dk, dv, segments, torch.float32)
+    noise = reference_noise(case, dk, dv, segments)
+    tol = max(2e-2, noise)
     q, kn, vn = (case[x][None].to(cuda) for x in ('q', 'k_new', 'v_new'))
     c.select(16)
     past = c.append(kn, vn, 0)
     one = c.attend(q, kn, vn, 0, past, out_dtype=torch.float32, segments=segments, path=path, splits=1,
                    precision='bf16')[0].cpu().double()
     err1 = (one - ref32).abs().max().item()
-    assert err1 <= 2e-2, err1
-    tol = 2e-2 + block_sensitivity(case, dk, dv, segments)
     got = c.attend(q, kn, vn, 0, past, out_dtype=torch.float32, segments=segments, path=path,
                    precision='bf16')[0].cpu().double()
     err = (got - ref32).abs().max().item()
-    assert err <= tol, (err, tol)
-    got = c.attend(q, kn, vn, 0, past, segments=segments, path=path, precision='bf16')[0].cpu().double()
+    got16 = c.attend(q, kn, vn, 0, past, segments=segments, path=path, precision='bf16')[0].cpu().double()
     ref = semantics_out(case, dk, dv, segments)
-    assert torch.all((got - ref).abs() <= tol + ref.abs() * 2.0 ** -7)
+    err16 = ((got16 - ref).abs() - ref.abs() * 2.0 ** -7).max().item()
+    print(f'[bf16-vs-reference] {label} path={path}: max-abs one split {err1:.4e}, default splits {err:.4e}, '
+          f'bf16 out beyond one ulp {err16:.4e}; reference p-rounding noise {noise:.4e}', flush=True)
+    assert err1 <= tol, (err1, tol)
+    assert err <= tol, (err, tol)
+    assert err16 <= tol, (err16, tol)
 
 
 PATHS = ['mfma', 'vector']
@@ -135,7 +146,7 @@ def test_frame_chunk_bf16_semantics_within_2e2_of_reference(cuda, past, path):
     announce(f'attention frame chunk past={past} path={path} precision=bf16')
     case = frame_chunk_case(past, seed=past + 2)
     c, dk, dv = build(case, cuda)
-    assert_semantics(c, case, dk, dv, cuda, path)
+    assert_semantics(c, case, dk, dv, cuda, path, label=f'frame chunk past={past}')
 
 
 @pytest.mark.parametrize('path', PATHS)
@@ -144,7 +155,7 @@ def test_candidates_bf16_semantics_within_2e2_of_reference(cuda, bits, path):
     announce(f'attention candidates bits={bits} path={path} precision=bf16')
     case = candidate_case(bits, seed=3, past=6144)
     c, dk, dv = build(case, cuda)
-    assert_semantics(c, case, dk, dv, cuda, path, case['segments'])
+    assert_semantics(c, case, dk, dv, cuda, path, case['segments'], label=f'candidates {bits}-bit')
 
 
 def test_bf16_within_2e2_of_reference_semantics_on_unit_normal_data(cuda):
@@ -200,7 +211,7 @@ def test_more_splits_than_one_merge_pass(cuda, precision, path):
     """128 splits (one per 64-key unit at past 8128): the combine kernels take a row's splits 64 at
     a time and rescale their running (max, sum, O) between the two passes. Same bounds as the
     single-pass cases: fp32 within 1e-3 of the fp64 oracle, bf16 within 2e-2 of the emulated
-    reference plus its own 32-vs-64-key block sensitivity."""
+    reference."""
     announce(f'attention 128 splits precision={precision} path={path}')
     case = frame_chunk_case(8128, seed=9)
     c, dk, dv = build(case, cuda)
@@ -210,8 +221,10 @@ def test_more_splits_than_one_merge_pass(cuda, precision, path):
         assert err <= 1e-3, err
     else:
         err = (got - semantics_out(case, dk, dv, None, torch.float32)).abs().max().item()
-        tol = 2e-2 + block_sensitivity(case, dk, dv)
-        assert err <= tol, (err, tol)
+        noise = reference_noise(case, dk, dv)
+        print(f'[bf16-vs-reference] 128 splits past=8128 path={path}: max-abs {err:.4e}, '
+              f'reference p-rounding noise {noise:.4e}', flush=True)
+        assert err <= max(2e-2, noise), (err, noise)
 
 
 @pytest.mark.parametrize('path', PATHS)
@@ -335,9 +348,7 @@ def random_configs(count=24, seed=2024):
 @pytest.mark.parametrize('i,heads,group,nq,past,segments,precision,path', random_configs())
 def test_random_shapes_against_the_oracles(cuda, i, heads, group, nq, past, segments, precision, path):
     """fp32 precision within 1e-3 of the fp64 oracle; bf16 at one split within 2e-2 of the emulated
-    reference plus the reference's own 32-vs-64-key block sensitivity on the same input (the MFMA
-    kernel's two key groups each keep a running max over 32 keys of every unit, which rounds p like
-    the reference would at 32-key blocks), on unit-normal data with outlier channels."""
+    reference, on unit-normal data with outlier channels."""
     announce(f'attention random config {i}: heads={heads} group={group} nq={nq} past={past} '
              f'segments={segments} precision={precision} path={path}')
     case = frame_chunk_case(past, seed=100 + i, heads=heads, q_heads=heads * group, nq=nq)
@@ -355,4 +366,7 @@ def test_random_shapes_against_the_oracles(cuda, i, heads, group, nq, past, segm
                        precision='bf16')[0].cpu().double()
         ref = semantics_out(case, dk, dv, segments, torch.float32)
         err = (got - ref).abs().max().item()
-        assert err <= 2e-2 + block_sensitivity(case, dk, dv, segments), err
+        noise = reference_noise(case, dk, dv, segments)
+        print(f'[bf16-vs-reference] random config {i}: max-abs {err:.4e}, reference p-rounding noise '
+              f'{noise:.4e}', flush=True)
+        assert err <= max(2e-2, noise), (err, noise)

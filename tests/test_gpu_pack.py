@@ -116,7 +116,8 @@ def test_batched_volume_bitexact(cuda, layers, frames):
                         payload, meta = segment_rows(arena, seg, layer, kv, head, layers, heads)
                         assert np.array_equal(payload, ref_p[i, layer, head].numpy())
                         if bits < 16:
-                            assert np.array_equal(meta[:, 0], ref_off[i, layer, head].numpy())
+                            assert np.array_equal(meta[:, 0].view(np.uint32),
+                                                  ref_off[i, layer, head].numpy().view(np.uint32))
                             assert np.array_equal(meta[:, 1].view(np.uint32),
                                                   ref_sc[i, layer, head].numpy().view(np.uint32))
     tiles = c.tiles.cpu().numpy()[:frames]

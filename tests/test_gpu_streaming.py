@@ -17,6 +17,7 @@ import pytest
 import torch
 
 from conftest import announce
+from dkv.gpu_cache import GPUCache
 from dkv.streaming import StreamingDecoder, build_decoder
 
 pytestmark = pytest.mark.gpu
@@ -93,17 +94,20 @@ def test_mixed_width_ingest_tracks_the_schedule(cuda):
     assert torch.isfinite(logits).all()
 
 
+@pytest.mark.parametrize('precision', ['fp32', 'bf16'])
 @pytest.mark.parametrize('pipeline', [1, 2, 3, 8])
-def test_graph_replayed_ingest_matches_eager(cuda, pipeline):
+def test_graph_replayed_ingest_matches_eager(cuda, pipeline, precision):
     """Frames 2..n replay captured HIP graphs of the decoder forward (launches read their step
     parameters from the device, and the attention runs the splits the host plan would choose for
     the current history); with pipeline=k, k consecutive frames replay one graph of their
     forwards, each a layer behind the one before on its own stream. The cache bookkeeping, the
     packed bytes and the logits must equal the eager ingest's exactly, and a second request that
-    reuses the captured graphs on the reset cache must reproduce the first bit for bit."""
-    announce(f'streaming: graph-replayed ingest vs eager, two requests, pipeline={pipeline}')
+    reuses the captured graphs on the reset cache must reproduce the first bit for bit. (At bf16
+    precision a replayed chunk whose history runs one split of a launch sized for more must store
+    its output like a direct one-split call: the 16-token prefix over an empty history.)"""
+    announce(f'streaming: graph-replayed ingest vs eager, two requests, pipeline={pipeline}, precision={precision}')
     model = build_decoder(**SMALL, seed=12)
-    dec = StreamingDecoder(model, precision='fp32', pipeline=pipeline)
+    dec = StreamingDecoder(model, precision=precision, pipeline=pipeline)
     g = torch.Generator().manual_seed(13)
     prefix = torch.randint(0, 512, (1, 16), generator=g)
     question = torch.randint(0, 512, (1, 24), generator=g)
@@ -229,3 +233,125 @@ def test_label_protocol_and_calibration_prior(cuda):
     dec.forward(bare, ids=prefix)
     torch.cuda.synchronize()
     assert torch.equal(prior, dec.answer(bare, question, cands))
+
+
+def test_compat_update_returns_dequantized_history_and_the_native_chunk(cuda):
+    """GPUCache.update (the HF Cache.update compat path, src/gpu_cache.py:114-119): append, then
+    return (k, v) [1, H, seen, 64] whose earlier rows are the dequantized history materialize()
+    returns and whose last n rows are the native chunk, bit for bit, at every width."""
+    announce('compat: GPUCache.update rows')
+    torch.manual_seed(51)
+    c = GPUCache(None, layers=2, heads=5, max_tokens=1024, backend='sdpa')
+    seen = 0
+    for bits, n in [(4, 64), (8, 37), (16, 64), (4, 1), (8, 90)]:
+        k = torch.randn(1, 5, n, 64, device=cuda, dtype=torch.bfloat16)
+        v = torch.randn(1, n, 5, 64, device=cuda, dtype=torch.bfloat16).transpose(1, 2)  # strided V
+        c.select(bits)
+        for layer in range(2):
+            rk, rv = c.update(k, v, layer)
+            assert rk.shape == rv.shape == (1, 5, seen + n, 64) and rk.dtype == torch.bfloat16
+            hk, hv = c.materialize(layer)
+            assert torch.equal(rk[:, :, :seen], hk[:, :, :seen]) and torch.equal(rv[:, :, :seen], hv[:, :, :seen])
+            assert torch.equal(rk[:, :, seen:], k) and torch.equal(rv[:, :, seen:], v)
+            if bits < 16:  # the cache itself holds the quantized rows; update() hands back the native ones
+                assert not torch.equal(hk[:, :, seen:], k)
+        seen += n
+    assert c.get_seq_length() == seen
+
+
+def test_sdpa_backend_decoder_matches_native_and_fused(cuda):
+    """The decoder on GPUCache(backend='sdpa'): install_packed_attention falls through to the
+    upstream attention forward, which calls GPUCache.update and runs SDPA on the returned K/V
+    (src/gpu_cache.py:174-178, the reference's 'reconstruct' mode, src/streaming.py:165).
+    All-16-bit: the K/V are the native ones bit for bit, so logits equal native DynamicCache's
+    within 0.05 (the 16-bit case of test_packed_16bit_matches_native_decoder). Mixed widths: within
+    0.3 of the fused packed backend on the same schedule (the reference's fused-vs-native score
+    bound, scripts/gpu_model_smoke.py:23-24)."""
+    announce('compat: backend=sdpa decoder vs native and fused')
+    model = build_decoder(**SMALL, seed=52)
+    g = torch.Generator().manual_seed(53)
+    prefix = torch.randint(0, 512, (1, 16), generator=g)
+    question = torch.randint(0, 512, (1, 24), generator=g)
+    frames = frames_for(model, 4, seed=54)
+    dec = StreamingDecoder(model)
+    ref = native_logits(model, prefix, frames, question)
+    total = 16 + 4 * 64 + 24 + 64
+    sdpa = dec.ingest(prefix, frames, [16] * 4, cache=dec.create_cache(total, backend='sdpa'))
+    got = dec.forward(sdpa, ids=question, logits=question.shape[1])
+    torch.cuda.synchronize()
+    assert sdpa.get_seq_length() == 16 + 4 * 64 + 24
+    err = (got - ref).abs().max().item()
+    print(f'[compat] sdpa backend 16-bit vs native: max-abs {err:.4e}', flush=True)
+    assert err <= 0.05, err
+    bits = [4, 8, 16, 4]
+    mixed = dec.ingest(prefix, frames, bits, cache=dec.create_cache(total, backend='sdpa'))
+    got = dec.forward(mixed, ids=question, logits=question.shape[1])
+    fused = dec.ingest(prefix, frames, bits)
+    want = dec.forward(fused, ids=question, logits=question.shape[1])
+    torch.cuda.synchronize()
+    err = (got - want).abs().max().item()
+    print(f'[compat] sdpa backend mixed widths vs fused: max-abs {err:.4e}', flush=True)
+    assert torch.isfinite(got).all() and err <= 0.3, err
+
+
+FULL_FRAMES = 16
+
+
+def test_full_size_decoder_configuration(cuda):
+    """The metric's end-to-end decoder at its configured size (build_decoder() defaults: 32 layers,
+    hidden 960, 15 / 5 heads, SwiGLU 2560, vocab 49280) over 16 mixed-width frames
+    (src/streaming.py:168-237):
+      - pipelined graph replays (8 frames per group) ingest the cache bit for bit like eager
+        launches (arena bytes, bookkeeping, question logits);
+      - an all-16-bit packed cache at precision='fp32' gives question logits within 0.25 of native
+        DynamicCache + SDPA (32 layers of bf16 GEMMs and bf16 SDPA against the fp32-accurate packed
+        kernel; the 2-layer decoder holds 0.05);
+      - batched candidate scores equal one fork per candidate within 2e-2."""
+    announce('streaming: full-size decoder, 16 frames')
+    from dkv.workloads import bit_schedule, candidate_lengths
+    model = build_decoder(seed=0)
+    vocab = model.config.vocab_size
+    g = torch.Generator().manual_seed(61)
+    prefix = torch.randint(0, vocab, (1, 16), generator=g)
+    question = torch.randint(0, vocab, (1, 24), generator=g)
+    cands = [torch.randint(0, vocab, (1, n), generator=g) for n in candidate_lengths(0, 4)]
+    frames = frames_for(model, FULL_FRAMES, seed=62)
+    bits = bit_schedule(FULL_FRAMES, FULL_FRAMES)
+    assert set(bits) == {4, 8, 16}
+
+    dec = StreamingDecoder(model, pipeline=8)
+
+    def request():
+        cache = dec.ingest(prefix, frames, bits)
+        logits = dec.forward(cache.fork(), ids=question, logits=question.shape[1])
+        torch.cuda.synchronize()
+        return cache, logits
+
+    eager_cache, eager = request()
+    eager_arena = eager_cache.arena[:eager_cache.arena_used].clone()
+    eager_plan, eager_tiles = list(eager_cache.plan), eager_cache.tiles.clone()
+    dec.graphs = True
+    request()  # captures
+    graph_cache, replayed = request()
+    assert (64, 8) in dec._group_graphs
+    assert graph_cache.plan == eager_plan and graph_cache.seen == eager_cache.seen
+    assert torch.equal(graph_cache.arena[:graph_cache.arena_used], eager_arena)
+    assert torch.equal(graph_cache.tiles[:len(graph_cache.tile_starts)], eager_tiles[:len(graph_cache.tile_starts)])
+    assert torch.equal(replayed, eager), (replayed - eager).abs().max().item()
+
+    seq = dec.answer(graph_cache, question, cands)
+    bat = dec.answer_batched(graph_cache, question, cands)
+    torch.cuda.synchronize()
+    print(f'[full-size] batched vs per-fork candidate scores: {seq.tolist()} / {bat.tolist()}', flush=True)
+    assert (seq - bat).abs().max().item() <= 2e-2, (seq, bat)
+    dec.graphs = False
+
+    ref = native_logits(model, prefix, frames, question)
+    exact = StreamingDecoder(model, precision='fp32')
+    cache16 = exact.ingest(prefix, frames, [16] * FULL_FRAMES)
+    got = exact.forward(cache16, ids=question, logits=question.shape[1])
+    torch.cuda.synchronize()
+    err = (got - ref).abs().max().item()
+    print(f'[full-size] 16-bit packed (fp32) vs native logits: max-abs {err:.4e}, '
+          f'logit scale {ref.abs().max().item():.3f}', flush=True)
+    assert err <= 0.25, err
