@@ -15,6 +15,7 @@
 // value, well under the bf16 output's rounding, at half the partial traffic).
 // Softmax runs in base 2: x = score * scale * log2(e).
 #include "dkv_attn_common.h"
+#include <mutex>
 
 namespace dkv {
 
@@ -499,6 +500,60 @@ int launch_attn_vec(const dkv_attn_args& a, const Plan& p, float* part_o, float2
   return (int)hipGetLastError();
 }
 
+// The launches of one attention call whose split partials go to `ws` (at least
+// p.part_o_bytes + p.part_ml_bytes bytes, or unused for one split).
+static int launch_attend(const dkv_attn_args& a, const Plan& p, void* ws, hipStream_t s) {
+  float* part_o = static_cast<float*>(ws);
+  float2* part_ml = reinterpret_cast<float2*>(static_cast<char*>(ws) + p.part_o_bytes);
+  const int rc = p.path == 2 ? launch_attn_mfma(a, p, part_o, part_ml, s) : launch_attn_vec(a, p, part_o, part_ml, s);
+  if (rc) return rc;
+  if (p.splits > 1) {
+    const int R = (a.q_heads / a.heads) * a.nq;
+    if (p.precision == 1)
+      hipLaunchKernelGGL(combine_kernel, dim3((R + 3) / 4, a.heads), dim3(256), 0, s, a, p.splits, part_o,
+                         part_ml);
+    else
+      hipLaunchKernelGGL(combine_half_kernel, dim3((R + 3) / 4, a.heads), dim3(256), 0, s, a, p.splits, part_o,
+                         part_ml);
+  }
+  return (int)hipGetLastError();
+}
+
+// Scratch of dkv_attend_noalloc: the split partials of one call, in device
+// memory that is part of the library's code object, so no call allocates. Each
+// device holds its own copy at its own address until the process ends. Host
+// code never passes this name to a kernel (on the host it is only a handle to
+// the symbol): it looks the device address up with hipGetSymbolAddress, once
+// per device, and uses that. Every call on a device shares the one copy; the
+// kernels write every partial they later read, so nothing has to start at zero.
+constexpr int SCRATCH_DEVICES = 64;
+static __device__ __attribute__((aligned(256))) uint8_t scratch[DKV_NOALLOC_SCRATCH_BYTES];
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[SCRATCH_DEVICES];  // device address of `scratch` per device index
+
+static int scratch_address(void** ptr) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= SCRATCH_DEVICES) {
+    set_error("dkv_attend_noalloc: device index %d beyond %d", dev, SCRATCH_DEVICES);
+    return DKV_EINVAL;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!p) {
+      set_error("dkv_attend_noalloc: no device address for the scratch buffer");
+      return DKV_EINVAL;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return 0;
+}
+
 }  // namespace dkv
 
 using namespace dkv;
@@ -527,21 +582,29 @@ int dkv_attend(const dkv_attn_args* args, void* stream) {
               (long long)a.workspace_bytes);
     return DKV_EINVAL;
   }
-  float* part_o = static_cast<float*>(a.workspace);
-  float2* part_ml = reinterpret_cast<float2*>(static_cast<char*>(a.workspace) + p.part_o_bytes);
-  hipStream_t s = (hipStream_t)stream;
-  const int rc = p.path == 2 ? launch_attn_mfma(a, p, part_o, part_ml, s) : launch_attn_vec(a, p, part_o, part_ml, s);
-  if (rc) return rc;
-  if (p.splits > 1) {
-    const int R = (a.q_heads / a.heads) * a.nq;
-    if (p.precision == 1)
-      hipLaunchKernelGGL(combine_kernel, dim3((R + 3) / 4, a.heads), dim3(256), 0, s, a, p.splits, part_o,
-                         part_ml);
-    else
-      hipLaunchKernelGGL(combine_half_kernel, dim3((R + 3) / 4, a.heads), dim3(256), 0, s, a, p.splits, part_o,
-                         part_ml);
+  return launch_attend(a, p, a.workspace, (hipStream_t)stream);
+}
+
+int dkv_attend_noalloc(const dkv_attn_args* args, void* stream) {
+  clear_error();
+  if (!args) {
+    set_error("dkv_attend_noalloc: null args");
+    return DKV_EINVAL;
   }
-  return (int)hipGetLastError();
+  const dkv_attn_args& a = *args;
+  if (int rc = check_args(a)) return rc;
+  const Plan p = make_plan(a);
+  const int64_t need = p.part_o_bytes + p.part_ml_bytes;
+  if (need > DKV_NOALLOC_SCRATCH_BYTES) {
+    set_error("dkv_attend_noalloc: this call's split partials need %lld bytes, more than the %d-byte "
+              "scratch buffer (use dkv_attend with a workspace, or fewer splits)",
+              (long long)need, DKV_NOALLOC_SCRATCH_BYTES);
+    return DKV_EINVAL;
+  }
+  void* ws = nullptr;
+  if (need > 0)
+    if (int rc = scratch_address(&ws)) return rc;
+  return launch_attend(a, p, ws, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -14,6 +14,7 @@ from . import _build
 
 DKV_EINVAL = -1
 DKV_MAX_CHUNK_SEGS = 16
+DKV_NOALLOC_SCRATCH_BYTES = 16 << 20
 ABI_VERSION = 2
 
 
@@ -79,6 +80,7 @@ SIGNATURES = [
                                        ctypes.c_int32, ctypes.c_void_p]),
     ('dkv_attend_workspace_bytes', ctypes.c_int64, [ctypes.POINTER(AttnArgs)]),
     ('dkv_attend', ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
+    ('dkv_attend_noalloc', ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
     ('dkv_export', ctypes.c_int, [ctypes.POINTER(SegmentIO), ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32,
                                   ctypes.c_int32, ctypes.c_void_p]),
     ('dkv_import', ctypes.c_int, [ctypes.POINTER(SegmentIO), ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,

@@ -178,6 +178,22 @@ int64_t dkv_attend_workspace_bytes(const dkv_attn_args* args);
  * out 16-byte aligned with strides in multiples of 4 elements. */
 int dkv_attend(const dkv_attn_args* args, void* stream);
 
+/* dkv_attend without a workspace and without allocating: no counterpart in the
+ * reference. For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). The
+ * split partials go to a scratch buffer of DKV_NOALLOC_SCRATCH_BYTES that the
+ * library's code object holds on each device (resident until the process ends);
+ * args->workspace and args->workspace_bytes are ignored. Results equal
+ * dkv_attend's for the same arguments. A call whose partials need more than
+ * DKV_NOALLOC_SCRATCH_BYTES (dkv_attend_workspace_bytes) returns DKV_EINVAL
+ * without launching; the metric's shapes need at most 13 MB. The first call on
+ * a device looks the buffer's address up (hipGetSymbolAddress): make that call
+ * before capturing a graph. Calls share their device's buffer, so two calls on
+ * one device that may overlap in time (different streams) race; serialize them
+ * (one stream) or use dkv_attend with separate workspaces. */
+#define DKV_NOALLOC_SCRATCH_BYTES (16 << 20)
+int dkv_attend_noalloc(const dkv_attn_args* args, void* stream);
+
 /* Copy one segment out of the arena into the reference's PackedTensor buffers
  * (src/kv_quantization.py:12-77). Together with the host-side 64-byte header
  * and the 32-byte segment descriptor (src/cache_manager.py:9,53-58), this
