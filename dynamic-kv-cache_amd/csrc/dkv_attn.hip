@@ -245,7 +245,7 @@ attn_vec_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ part
 // on lane s and fetched with a shuffle. The 4 lanes of one chunk are summed at
 // the end, and lanes 0..15 store the row.
 __global__ void __launch_bounds__(256)
-combine_kernel(dkv_attn_args a, int splits, const float* __restrict__ part_o,
+combine_kernel(dkv_attn_args a, int splits, int short_plan, const float* __restrict__ part_o,
                const float2* __restrict__ part_ml) {
   const int h = blockIdx.y;
   const int G = a.q_heads / a.heads;
@@ -253,9 +253,10 @@ combine_kernel(dkv_attn_args a, int splits, const float* __restrict__ part_o,
   const int r = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (r >= R) return;
-  int units = 0;
+  int units = a.n_tiles + (a.nq + TILE - 1) / TILE;
   Hist hs;
-  const int active = runtime_plan(a, hs, units, splits);  // partials written (graph replays: fewer)
+  // partials written (graph replays: fewer), by the producing kernel's rule
+  const int active = short_plan ? short_runtime_plan(a, hs, units, splits) : runtime_plan(a, hs, units, splits);
   if (active <= 1) return;  // one split ran and stored the output itself
   const int64_t base = (int64_t)h * splits * R + r;
   const int j = lane >> 4, c = lane & 15;
@@ -317,7 +318,7 @@ combine_kernel(dkv_attn_args a, int splits, const float* __restrict__ part_o,
 // (fetched from lane s with a shuffle). The 8 lanes of one chunk are summed
 // at the end, and lanes 0..7 store the row.
 __global__ void __launch_bounds__(256)
-combine_half_kernel(dkv_attn_args a, int splits, const float* __restrict__ part_o,
+combine_half_kernel(dkv_attn_args a, int splits, int short_plan, const float* __restrict__ part_o,
                     const float2* __restrict__ part_ml) {
   const int h = blockIdx.y;
   const int G = a.q_heads / a.heads;
@@ -325,9 +326,10 @@ combine_half_kernel(dkv_attn_args a, int splits, const float* __restrict__ part_
   const int r = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (r >= R) return;
-  int units = 0;
+  int units = a.n_tiles + (a.nq + TILE - 1) / TILE;
   Hist hs;
-  const int active = runtime_plan(a, hs, units, splits);  // partials written (graph replays: fewer)
+  // partials written (graph replays: fewer), by the producing kernel's rule
+  const int active = short_plan ? short_runtime_plan(a, hs, units, splits) : runtime_plan(a, hs, units, splits);
   if (active <= 1) return;  // one split ran and stored the output itself
   const int64_t base = (int64_t)h * splits * R + r;
   const int j = lane >> 3, c = lane & 7;
@@ -434,8 +436,14 @@ static int check_args(const dkv_attn_args& a) {
         return DKV_EINVAL;
       }
   }
-  if (a.path < 0 || a.path > 2 || a.precision < 0 || a.precision > 1) {
-    set_error("dkv_attend: path must be 0 (auto), 1 (vector) or 2 (MFMA); precision 0 (bf16) or 1 (fp32)");
+  if (a.path < 0 || a.path > 3 || a.precision < 0 || a.precision > 1) {
+    set_error("dkv_attend: path must be 0 (auto), 1 (vector), 2 (MFMA) or 3 (short chunk); precision 0 (bf16) or "
+              "1 (fp32)");
+    return DKV_EINVAL;
+  }
+  if (a.path == 3 && (a.q_heads / a.heads) * a.nq > SHORT_ROWS) {
+    set_error("dkv_attend: the short-chunk path takes at most %d query rows per KV head (q_heads / heads * nq = %d)",
+              SHORT_ROWS, (a.q_heads / a.heads) * a.nq);
     return DKV_EINVAL;
   }
   if (a.out_dtype != 0 && a.out_dtype != 1) {
@@ -460,18 +468,20 @@ static Plan make_plan(const dkv_attn_args& a) {
   const int G = a.q_heads / a.heads;
   const int R = G * a.nq;
   p.path = a.path;
-  // Auto takes the MFMA kernel for every chunk length: even a one-token decode step (3 rows per
-  // KV head, 13 of every 16 MFMA rows idle) runs in half the vector kernel's time at long
-  // histories, because the MFMA kernel's unit pipeline is what bounds both.
-  if (p.path == 0) p.path = 2;
+  // Auto: the short-chunk kernel when every query row of a KV head fits one 16-row MFMA block
+  // (decode steps), the frame-chunk MFMA kernel otherwise.
+  if (p.path == 0) p.path = R <= SHORT_ROWS ? 3 : 2;
   p.precision = a.precision;
-  p.rows_per_group = p.path == 2 ? MFMA_ROWS : VEC_ROWS;
+  p.rows_per_group = p.path == 3 ? SHORT_ROWS : (p.path == 2 ? MFMA_ROWS : VEC_ROWS);
   p.row_groups = (R + p.rows_per_group - 1) / p.rows_per_group;
   p.units = a.n_tiles + (a.nq + TILE - 1) / TILE;
   int splits = a.splits;
   if (splits <= 0) {
     const int per = a.heads * p.row_groups;
-    if (p.path == 2) {
+    if (p.path == 3) {
+      // one wave per unit: every tile of the history is requested when the kernel starts
+      splits = (p.units + SHORT_UNITS - 1) / SHORT_UNITS;
+    } else if (p.path == 2) {
       // One 8-wave workgroup per CU, all resident at once: a grid one past
       // the CU count would take a second round for a single workgroup.
       splits = num_cus() / per;
@@ -483,8 +493,13 @@ static Plan make_plan(const dkv_attn_args& a) {
   if (splits < 1) splits = 1;
   p.splits = splits;
   if (splits > 1) {
-    p.part_o_bytes = (int64_t)a.heads * splits * R * D * (p.precision ? 4 : 2);  // fp32 O or fp16 O / sum
-    p.part_ml_bytes = (int64_t)a.heads * splits * R * 8;
+    if (p.path == 3) {  // unnormalized fp32 O and (max, sum), as combine_kernel reads them
+      p.part_o_bytes = (int64_t)a.heads * splits * R * D * 4;
+      p.part_ml_bytes = (int64_t)a.heads * splits * R * 8;
+    } else {
+      p.part_o_bytes = (int64_t)a.heads * splits * R * D * (p.precision ? 4 : 2);  // fp32 O or fp16 O / sum
+      p.part_ml_bytes = (int64_t)a.heads * splits * R * 8;
+    }
   } else {
     p.part_o_bytes = p.part_ml_bytes = 0;
   }
@@ -505,16 +520,19 @@ int launch_attn_vec(const dkv_attn_args& a, const Plan& p, float* part_o, float2
 static int launch_attend(const dkv_attn_args& a, const Plan& p, void* ws, hipStream_t s) {
   float* part_o = static_cast<float*>(ws);
   float2* part_ml = reinterpret_cast<float2*>(static_cast<char*>(ws) + p.part_o_bytes);
-  const int rc = p.path == 2 ? launch_attn_mfma(a, p, part_o, part_ml, s) : launch_attn_vec(a, p, part_o, part_ml, s);
+  const int rc = p.path == 3 ? launch_attn_short(a, p, part_o, part_ml, s)
+                 : p.path == 2 ? launch_attn_mfma(a, p, part_o, part_ml, s)
+                               : launch_attn_vec(a, p, part_o, part_ml, s);
   if (rc) return rc;
   if (p.splits > 1) {
     const int R = (a.q_heads / a.heads) * a.nq;
-    if (p.precision == 1)
-      hipLaunchKernelGGL(combine_kernel, dim3((R + 3) / 4, a.heads), dim3(256), 0, s, a, p.splits, part_o,
-                         part_ml);
+    const int short_plan = p.path == 3;
+    if (p.precision == 1 || short_plan)  // the short-chunk kernel's partials are fp32 in both precisions
+      hipLaunchKernelGGL(combine_kernel, dim3((R + 3) / 4, a.heads), dim3(256), 0, s, a, p.splits, short_plan,
+                         part_o, part_ml);
     else
-      hipLaunchKernelGGL(combine_half_kernel, dim3((R + 3) / 4, a.heads), dim3(256), 0, s, a, p.splits, part_o,
-                         part_ml);
+      hipLaunchKernelGGL(combine_half_kernel, dim3((R + 3) / 4, a.heads), dim3(256), 0, s, a, p.splits, short_plan,
+                         part_o, part_ml);
   }
   return (int)hipGetLastError();
 }

@@ -9,6 +9,27 @@ namespace dkv {
 
 constexpr float LOG2E = 1.4426950408889634f;
 
+// Timeline probe, a build option (-DDKV_TIMELINE; off in the library build):
+// lane 0 of each workgroup records wall_clock64() (a 100 MHz counter shared by
+// all CUs) at numbered points of a kernel into its source file's device array,
+// which that build's dkv_timeline_*() export copies out. Used to see where a
+// launch's time goes (which memory round trips sit on the critical path).
+#ifdef DKV_TIMELINE
+constexpr int TL_EVENTS = 8;
+constexpr int TL_SLOTS = 1 << 14;  // workgroups recorded per launch
+#define DKV_TL(buf, ev)                                                                        \
+  do {                                                                                         \
+    if (threadIdx.x == 0) {                                                                    \
+      const int tl_wg = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);        \
+      if (tl_wg < TL_SLOTS) buf[tl_wg * TL_EVENTS + (ev)] = wall_clock64();                    \
+    }                                                                                          \
+  } while (0)
+#else
+#define DKV_TL(buf, ev) \
+  do {                  \
+  } while (0)
+#endif
+
 // A unit is 64 keys of one KV head: a history tile of the arena, or a 64-row
 // piece of the chunk's own native K/V.
 struct Unit {
@@ -69,6 +90,14 @@ __device__ __forceinline__ int runtime_plan(const dkv_attn_args& a, Hist& hs, in
   return min(splits, units);
 }
 
+// The same for the short-chunk kernel, whose default split count is
+// ceil(units / SHORT_UNITS) workgroups per KV head rather than the launch's
+// count: the splits that run for the runtime history are the ones a direct
+// call on that history runs (an explicit args.splits keeps its meaning), never
+// more than the launch's grid (nwg). The merge kernel that reads the short
+// kernel's partials applies the same rule.
+__device__ __forceinline__ int short_runtime_plan(const dkv_attn_args& a, Hist& hs, int& units, int nwg);
+
 // First chunk row of the segment holding chunk row j (0 when n_segs <= 1).
 __device__ __forceinline__ int chunk_seg_start(const dkv_attn_args& a, int j) {
   int start = 0;
@@ -80,8 +109,10 @@ __device__ __forceinline__ int chunk_seg_start(const dkv_attn_args& a, int j) {
 // Workspace of a split call: partial outputs [heads, splits, R, 64] (fp32 O
 // for precision 1, fp16 O / sum for precision 0), then partial (max, sum)
 // [heads, splits, R] float2.
+// The short-chunk kernel writes fp32 partials (precision-1 layout) in both
+// precisions.
 struct Plan {
-  int path;       // 1 vector, 2 MFMA
+  int path;       // 1 vector, 2 MFMA, 3 short chunk
   int precision;  // 0 bf16 operands (reference rounding), 1 fp32-accurate
   int units;
   int splits;
@@ -95,8 +126,23 @@ int launch_attn_vec(const dkv_attn_args& a, const Plan& p, float* part_o, float2
                     hipStream_t s);
 int launch_attn_mfma(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml,
                      hipStream_t s);
+int launch_attn_short(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml, hipStream_t s);
 
+constexpr int SHORT_ROWS = 16;  // query rows per KV head the short-chunk kernel takes (one MFMA block)
+constexpr int SHORT_UNITS = 4;  // 64-key units per short-chunk workgroup (one per wave) by default
 constexpr int VEC_ROWS = 64;    // query rows per vector-path workgroup
+
+__device__ __forceinline__ int short_runtime_plan(const dkv_attn_args& a, Hist& hs, int& units, int nwg) {
+  hs.past = a.past;
+  hs.n_tiles = a.n_tiles;
+  if (a.step) {
+    hs.past = a.step[0];
+    hs.n_tiles = a.step[1];
+    units = hs.n_tiles + (a.nq + TILE - 1) / TILE;
+  }
+  const int want = a.splits > 0 ? min(a.splits, units) : (units + SHORT_UNITS - 1) / SHORT_UNITS;
+  return max(1, min(nwg, want));
+}
 constexpr int MFMA_ROWS = 192;  // query rows per MFMA-path workgroup (4 waves x 3 x 16)
 
 // Precision-0 split partials hold O / sum in fp16, 64 values per row (128

@@ -29,7 +29,7 @@ BITS = (4, 8, 16)
 # 'bf16': dequantized K/V and p rounded to bf16 before the dot products, as the reference kernel
 # does (src/gpu_kernels.py:93-94,102). 'fp32': fp32-accurate (split bf16 pairs on the MFMA path).
 PRECISIONS = {'bf16': 0, 'fp32': 1}
-PATHS = {'auto': 0, 'vector': 1, 'mfma': 2}
+PATHS = {'auto': 0, 'vector': 1, 'mfma': 2, 'short': 3}
 
 
 # The kernels store bf16 or fp32 (dkv_attn_args.out_dtype, dkv_reconstruct's out_dtype); any other
@@ -399,9 +399,10 @@ class GPUCache(_CacheBase):
         """Causal attention of q over history [0, past) plus the native chunk (src/gpu_cache.py:96-104).
 
         `segments` (optional) lists chunk boundaries [0, b1, ..., nq] for a block-diagonal batch of
-        independent continuations that share the history, e.g. QA candidates. `path` is 'auto'
-        (the MFMA kernel for every chunk length), 'vector' or 'mfma'; `precision` overrides the
-        cache's 'bf16' / 'fp32' setting for this call.
+        independent continuations that share the history, e.g. QA candidates. `path` is 'auto' (the
+        short-chunk kernel when q_heads / heads * n <= 16, e.g. decode steps, else the frame-chunk
+        MFMA kernel), 'short', 'mfma' or 'vector'; `precision` overrides the cache's 'bf16' / 'fp32'
+        setting for this call.
         """
         if precision is not None and precision not in PRECISIONS:
             raise ValueError(f'precision must be one of {sorted(PRECISIONS)}')

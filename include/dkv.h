@@ -88,7 +88,8 @@ typedef struct dkv_attn_args {
   void* out;             /* [nq, q_heads, 64] with the strides below */
   int64_t out_tok_stride, out_head_stride;
   int32_t out_dtype;     /* 0 = bf16, 1 = fp32 */
-  int32_t path;          /* 0 = auto (the MFMA kernel), 1 = vector, 2 = MFMA */
+  int32_t path;          /* 0 = auto (short chunk when q_heads / heads * nq <= 16, else MFMA),
+                            1 = vector, 2 = MFMA (frame chunks), 3 = short chunk (decode steps) */
   int32_t splits;        /* 0 = auto; history split count per KV head */
   int32_t precision;     /* 0 = the reference kernel's bf16 rounding of K, V and p
                             (src/gpu_kernels.py:93-94,102); 1 = fp32-accurate */
@@ -172,6 +173,9 @@ int64_t dkv_attend_workspace_bytes(const dkv_attn_args* args);
 
 /* Fused packed-history causal GQA attention. Replaces GPUCache.attend's
  * packed_attention launch (src/gpu_cache.py:96-104, src/gpu_kernels.py:71-105).
+ * Frame chunks run a split-history MFMA kernel, short chunks (at most 16 query
+ * rows per KV head, e.g. decode steps) a kernel with one wave per 64-key tile;
+ * a merge kernel combines the history splits of either.
  * Output rows are written to out + m*out_tok_stride + qh*out_head_stride
  * (elements), the reference's [1, nq, q_heads, 64] layout when contiguous.
  * Q, K and V must be 16-byte aligned with strides in multiples of 8 elements;

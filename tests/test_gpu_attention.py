@@ -370,3 +370,115 @@ def test_random_shapes_against_the_oracles(cuda, i, heads, group, nq, past, segm
         print(f'[bf16-vs-reference] random config {i}: max-abs {err:.4e}, reference p-rounding noise '
               f'{noise:.4e}', flush=True)
         assert err <= max(2e-2, noise), (err, noise)
+
+
+# -- the short-chunk kernel (decode steps: q_heads / heads * nq <= 16) ---------------------------
+@pytest.mark.parametrize('precision', ['fp32', 'bf16'])
+@pytest.mark.parametrize('past,nq', [(0, 1), (1, 1), (63, 4), (64, 5), (700, 1), (1000, 3), (8128, 1), (8128, 4)])
+def test_short_chunk_kernel(cuda, past, nq, precision):
+    """The short-chunk kernel (one wave per 64-key unit, splits merged by the last workgroup in the
+    same launch) against the oracles: fp32 precision within 1e-3 of the fp64 oracle, bf16 within
+    max(2e-2, the reference's own p-rounding noise) of the emulated reference; and equal to the
+    frame-chunk MFMA kernel's result on the same call within those bounds."""
+    announce(f'attention short path past={past} nq={nq} precision={precision}')
+    case = frame_chunk_case(past, seed=300 + past + nq, nq=nq)
+    c, dk, dv = build(case, cuda)
+    got = run(c, case, cuda, torch.float32, path='short', precision=precision)
+    if precision == 'fp32':
+        err = (got - oracle_out(case, dk, dv)).abs().max().item()
+        assert err <= 1e-3, err
+    else:
+        noise = reference_noise(case, dk, dv)
+        err = (got - semantics_out(case, dk, dv, None, torch.float32)).abs().max().item()
+        print(f'[bf16-vs-reference] short path past={past} nq={nq}: max-abs {err:.4e}, noise {noise:.4e}', flush=True)
+        assert err <= max(2e-2, noise), (err, noise)
+
+
+@pytest.mark.parametrize('splits', [1, 2, 3, 7, 1000])
+@pytest.mark.parametrize('precision', ['fp32', 'bf16'])
+def test_short_chunk_split_counts(cuda, splits, precision):
+    """Explicit split counts (workgroups per KV head): 1 stores the output directly, 1000 puts one
+    unit per workgroup (several waves idle); consecutive calls on one workspace agree bit for bit."""
+    announce(f'attention short path splits={splits} precision={precision}')
+    case = frame_chunk_case(2000, seed=7, nq=4)
+    c, dk, dv = build(case, cuda)
+    ref = oracle_out(case, dk, dv) if precision == 'fp32' else semantics_out(case, dk, dv, None, torch.float32)
+    tol = 1e-3 if precision == 'fp32' else max(2e-2, reference_noise(case, dk, dv))
+    q, kn, vn = (case[x][None].to(cuda) for x in ('q', 'k_new', 'v_new'))
+    c.select(16)
+    past = c.append(kn, vn, 0)
+    outs = [c.attend(q, kn, vn, 0, past, out_dtype=torch.float32, path='short', splits=splits, precision=precision)
+            for _ in range(3)]
+    torch.cuda.synchronize()
+    for o in outs:
+        assert (o[0].cpu().double() - ref).abs().max().item() <= tol
+        assert torch.equal(o, outs[0])
+    if splits == 1:  # one split needs no workspace at all
+        assert c._workspace is None
+
+
+@pytest.mark.parametrize('bits', [4, 8])
+def test_short_chunk_segments(cuda, bits):
+    """Short chunk with a block-diagonal mask: 5 one-token continuations of one history (15 rows)."""
+    announce(f'attention short path segments bits={bits}')
+    case = candidate_case(bits, seed=11, past=1536, count=4)
+    n = case['q'].shape[1]
+    case = dict(case, q=case['q'][:, :5], k_new=case['k_new'][:, :5], v_new=case['v_new'][:, :5])
+    segments = [0, 1, 2, 3, 4, 5]
+    c, dk, dv = build(case, cuda)
+    got = run(c, case, cuda, torch.float32, segments=segments, path='short')
+    assert n >= 5
+    assert (got - oracle_out(case, dk, dv, segments)).abs().max().item() <= 1e-3
+
+
+def test_short_chunk_rejects_too_many_rows(cuda):
+    case = frame_chunk_case(128, seed=1, nq=6)  # 3 x 6 = 18 rows per KV head
+    c, _, _ = build(case, cuda)
+    q, kn, vn = (case[x][None].to(cuda) for x in ('q', 'k_new', 'v_new'))
+    c.select(16)
+    past = c.append(kn, vn, 0)
+    with pytest.raises(ValueError, match='short-chunk'):
+        c.attend(q, kn, vn, 0, past, path='short')
+
+
+@pytest.mark.parametrize('precision', ['fp32', 'bf16'])
+def test_decode_steps_replayed_from_a_graph(cuda, precision):
+    """One-token decode steps recorded once in a HIP graph (the launch sized for the cache's
+    capacity, the history read from the device step pair) and replayed as the history grows from 0
+    to 9 tiles: every replay must equal a direct call on the same history bit for bit."""
+    announce(f'attention decode steps graph replay precision={precision}')
+    torch.manual_seed(5)
+    heads, q_heads = 5, 15
+    c = GPUCache(None, layers=1, heads=heads, max_tokens=640, precision=precision)
+    q = torch.randn(1, q_heads, 1, 64, device=cuda, dtype=torch.bfloat16)
+    kn = torch.randn(1, heads, 1, 64, device=cuda, dtype=torch.bfloat16)
+    vn = torch.randn(1, heads, 1, 64, device=cuda, dtype=torch.bfloat16)
+    steps = c.begin_graph_steps(1, q_heads=q_heads)
+    c.select(16)
+    c.graph_step()
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        c.attend(q, kn, vn, 0, 0)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = c.attend(q, kn, vn, 0, 0)
+    c.end_graph_steps()
+    c.reset()
+    bits = [4, 8, 16, 4, 8, 4, 16, 8, 4]
+    for i in range(len(bits) + 1):
+        past = c.seen[0]
+        c.begin_graph_steps(1, steps=steps)
+        c.graph_step()  # opens a one-token segment at the pending width and uploads {past, n_tiles}
+        graph.replay()
+        c.end_graph_steps()
+        got = out.clone()
+        c.seen = [past]  # the direct call on the same history (the step's token not appended)
+        ref = c.attend(q, kn, vn, 0, past)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), (i, (got.float() - ref.float()).abs().max().item())
+        c.seen = [past + 1]
+        if i < len(bits):  # grow the history by a 63-token segment at the next width
+            c.select(bits[i])
+            c.append(torch.randn(1, heads, 63, 64, device=cuda, dtype=torch.bfloat16),
+                     torch.randn(1, heads, 63, 64, device=cuda, dtype=torch.bfloat16), 0)
