@@ -92,7 +92,7 @@ constexpr int VEC_RPW = VEC_ROWS / 4;
 
 template <int PREC>
 __global__ void __launch_bounds__(ATT_THREADS)
-attn_vec_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ part_o,
+attn_vec_kernel(dkv_attn_args a, int units, int splits, int cap, float* __restrict__ part_o,
                 float2* __restrict__ part_ml) {
   __shared__ float Qs[VEC_ROWS][D];
   __shared__ float Kt[TILE][D + 1];
@@ -100,7 +100,7 @@ attn_vec_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ part
   __shared__ float Ps[4][TILE];
 
   Hist hs;
-  const int active = runtime_plan(a, hs, units, splits);
+  const int active = runtime_plan(a, hs, units, splits, cap);
   const int split = blockIdx.x, h = blockIdx.y, rg = blockIdx.z;
   const int G = a.q_heads / a.heads;
   const int R = G * a.nq;
@@ -245,7 +245,7 @@ attn_vec_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ part
 // on lane s and fetched with a shuffle. The 4 lanes of one chunk are summed at
 // the end, and lanes 0..15 store the row.
 __global__ void __launch_bounds__(256)
-combine_kernel(dkv_attn_args a, int splits, int short_plan, const float* __restrict__ part_o,
+combine_kernel(dkv_attn_args a, int splits, int cap, int short_plan, const float* __restrict__ part_o,
                const float2* __restrict__ part_ml) {
   const int h = blockIdx.y;
   const int G = a.q_heads / a.heads;
@@ -256,7 +256,7 @@ combine_kernel(dkv_attn_args a, int splits, int short_plan, const float* __restr
   int units = a.n_tiles + (a.nq + TILE - 1) / TILE;
   Hist hs;
   // partials written (graph replays: fewer), by the producing kernel's rule
-  const int active = short_plan ? short_runtime_plan(a, hs, units, splits) : runtime_plan(a, hs, units, splits);
+  const int active = short_plan ? short_runtime_plan(a, hs, units, splits) : runtime_plan(a, hs, units, splits, cap);
   if (active <= 1) return;  // one split ran and stored the output itself
   const int64_t base = (int64_t)h * splits * R + r;
   const int j = lane >> 4, c = lane & 15;
@@ -318,7 +318,7 @@ combine_kernel(dkv_attn_args a, int splits, int short_plan, const float* __restr
 // (fetched from lane s with a shuffle). The 8 lanes of one chunk are summed
 // at the end, and lanes 0..7 store the row.
 __global__ void __launch_bounds__(256)
-combine_half_kernel(dkv_attn_args a, int splits, int short_plan, const float* __restrict__ part_o,
+combine_half_kernel(dkv_attn_args a, int splits, int cap, int short_plan, const float* __restrict__ part_o,
                     const float2* __restrict__ part_ml) {
   const int h = blockIdx.y;
   const int G = a.q_heads / a.heads;
@@ -329,7 +329,7 @@ combine_half_kernel(dkv_attn_args a, int splits, int short_plan, const float* __
   int units = a.n_tiles + (a.nq + TILE - 1) / TILE;
   Hist hs;
   // partials written (graph replays: fewer), by the producing kernel's rule
-  const int active = short_plan ? short_runtime_plan(a, hs, units, splits) : runtime_plan(a, hs, units, splits);
+  const int active = short_plan ? short_runtime_plan(a, hs, units, splits) : runtime_plan(a, hs, units, splits, cap);
   if (active <= 1) return;  // one split ran and stored the output itself
   const int64_t base = (int64_t)h * splits * R + r;
   const int j = lane >> 3, c = lane & 7;
@@ -476,17 +476,21 @@ static Plan make_plan(const dkv_attn_args& a) {
   p.row_groups = (R + p.rows_per_group - 1) / p.rows_per_group;
   p.units = a.n_tiles + (a.nq + TILE - 1) / TILE;
   int splits = a.splits;
+  p.cap = 0;
   if (splits <= 0) {
     const int per = a.heads * p.row_groups;
     if (p.path == 3) {
-      // one wave per unit: every tile of the history is requested when the kernel starts
+      // two waves per unit, four units per workgroup: every tile of the history is requested
+      // when the kernel starts
       splits = (p.units + SHORT_UNITS - 1) / SHORT_UNITS;
-    } else if (p.path == 2) {
-      // One 8-wave workgroup per CU, all resident at once: a grid one past
-      // the CU count would take a second round for a single workgroup.
-      splits = num_cus() / per;
     } else {
-      splits = (2 * num_cus() + per - 1) / per;
+      // MFMA: one 8-wave workgroup per CU, all resident at once (a grid one past the CU count
+      // would take a second round for a single workgroup); balanced over the history. A launch
+      // that reads its history from a device step pair (graph replays) is sized for the cap,
+      // the most splits any history runs.
+      p.cap = p.path == 2 ? num_cus() / per : (2 * num_cus() + per - 1) / per;
+      if (p.cap < 1) p.cap = 1;
+      splits = a.step ? p.cap : balanced_splits(p.units, p.cap);
     }
   }
   if (splits > p.units) splits = p.units;
@@ -509,9 +513,11 @@ static Plan make_plan(const dkv_attn_args& a) {
 int launch_attn_vec(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml, hipStream_t s) {
   const dim3 grid(p.splits, a.heads, p.row_groups);
   if (p.precision == 1)
-    hipLaunchKernelGGL(attn_vec_kernel<1>, grid, dim3(ATT_THREADS), 0, s, a, p.units, p.splits, part_o, part_ml);
+    hipLaunchKernelGGL(attn_vec_kernel<1>, grid, dim3(ATT_THREADS), 0, s, a, p.units, p.splits, p.cap, part_o,
+                       part_ml);
   else
-    hipLaunchKernelGGL(attn_vec_kernel<0>, grid, dim3(ATT_THREADS), 0, s, a, p.units, p.splits, part_o, part_ml);
+    hipLaunchKernelGGL(attn_vec_kernel<0>, grid, dim3(ATT_THREADS), 0, s, a, p.units, p.splits, p.cap, part_o,
+                       part_ml);
   return (int)hipGetLastError();
 }
 
@@ -528,11 +534,11 @@ static int launch_attend(const dkv_attn_args& a, const Plan& p, void* ws, hipStr
     const int R = (a.q_heads / a.heads) * a.nq;
     const int short_plan = p.path == 3;
     if (p.precision == 1 || short_plan)  // the short-chunk kernel's partials are fp32 in both precisions
-      hipLaunchKernelGGL(combine_kernel, dim3((R + 3) / 4, a.heads), dim3(256), 0, s, a, p.splits, short_plan,
-                         part_o, part_ml);
+      hipLaunchKernelGGL(combine_kernel, dim3((R + 3) / 4, a.heads), dim3(256), 0, s, a, p.splits, p.cap,
+                         short_plan, part_o, part_ml);
     else
-      hipLaunchKernelGGL(combine_half_kernel, dim3((R + 3) / 4, a.heads), dim3(256), 0, s, a, p.splits, short_plan,
-                         part_o, part_ml);
+      hipLaunchKernelGGL(combine_half_kernel, dim3((R + 3) / 4, a.heads), dim3(256), 0, s, a, p.splits, p.cap,
+                         short_plan, part_o, part_ml);
   }
   return (int)hipGetLastError();
 }

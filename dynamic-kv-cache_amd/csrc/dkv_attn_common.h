@@ -74,20 +74,33 @@ __device__ __forceinline__ Unit get_unit(const dkv_attn_args& a, const Hist& hs,
   return un;
 }
 
+// The default split count of a history of `units` units: at most `cap` splits
+// (the count that keeps every workgroup resident), each of at most
+// ceil(units / cap) units, and no more splits than that needs. So the
+// critical path is as short as with `cap` splits while the partials (and the
+// merge's reads) shrink: 65 units at cap 51 run as 33 splits of two units.
+__host__ __device__ inline int balanced_splits(int units, int cap) {
+  if (units <= cap) return units < 1 ? 1 : units;
+  const int per = (units + cap - 1) / cap;
+  return (units + per - 1) / per;
+}
+
 // Graph replays: the history bounds the kernels run with come from the device
 // step pair when one is given, and the launch-time `units` and `splits` are
-// bounds only. The splits that run are then min(splits, units), as the host
-// plan would choose for the same history, so a replay partitions the history
-// exactly like a direct call; the other workgroups exit at once and the
-// partials keep the launch's split stride. Returns the splits that run.
-__device__ __forceinline__ int runtime_plan(const dkv_attn_args& a, Hist& hs, int& units, int splits) {
+// bounds only (such launches are sized for `cap` splits). The splits that run
+// are then the ones a direct call on the same history runs,
+// balanced_splits(units, cap), or min(explicit splits, units) when the caller
+// chose the count (cap 0), so a replay partitions the history exactly like a
+// direct call; the other workgroups exit at once and the partials keep the
+// launch's split stride. Returns the splits that run.
+__device__ __forceinline__ int runtime_plan(const dkv_attn_args& a, Hist& hs, int& units, int splits, int cap) {
   hs.past = a.past;
   hs.n_tiles = a.n_tiles;
   if (!a.step) return splits;
   hs.past = a.step[0];
   hs.n_tiles = a.step[1];
   units = hs.n_tiles + (a.nq + TILE - 1) / TILE;
-  return min(splits, units);
+  return min(splits, cap > 0 ? balanced_splits(units, cap) : units);
 }
 
 // The same for the short-chunk kernel, whose default split count is
@@ -118,6 +131,7 @@ struct Plan {
   int splits;
   int row_groups;
   int rows_per_group;
+  int cap;        // default split cap (0: the caller's explicit split count)
   int64_t part_o_bytes, part_ml_bytes;
 };
 

@@ -181,9 +181,15 @@ __device__ __forceinline__ Unit unit_at(const dkv_attn_args& a, const Hist& hs, 
 // block is past the last row skips the MFMA work (a scalar branch); other
 // waves compute all NBW blocks, those past the last row on zero queries, and
 // store only real rows.
+#ifdef DKV_TIMELINE
+// events: 0 entry, 1 first unit staged in LDS, 2 first unit dequantized, 3 first unit computed,
+// 4 last unit computed, 5 key groups merged, 6 stores issued
+static __device__ uint64_t tl_mfma[TL_SLOTS * TL_EVENTS];
+#endif
+
 template <int PREC, int NBW>
 __global__ void __launch_bounds__(MF_THREADS)
-attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ part_o,
+attn_mfma_kernel(dkv_attn_args a, int units, int splits, int cap, float* __restrict__ part_o,
                  float2* __restrict__ part_ml) {
   // LDS: two raw stages of (K, V) sub-blocks and two sets of bf16 tiles
   // (K, V^T, and for PREC 1 their lo parts). After the last unit the same
@@ -197,8 +203,9 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ par
   auto raw_buf = [&](int st, int kv) { return smem + (st * 2 + kv) * RAWP; };
   auto tile = [&](int b, int which) { return reinterpret_cast<uint16_t*>(smem + RAW_BYTES + (b * NT + which) * TILE_BYTES); };
 
+  DKV_TL(tl_mfma, 0);
   Hist hs;
-  const int active = runtime_plan(a, hs, units, splits);
+  const int active = runtime_plan(a, hs, units, splits, cap);
   const int split = blockIdx.x, h = blockIdx.y, rg = blockIdx.z;
   const int G = a.q_heads / a.heads;
   const int R = G * a.nq;
@@ -450,8 +457,10 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ par
   if (n > 0) raw_load(a, unit(0), h, wk0, wv0);
   if (n > 1) raw_load(a, unit(1), h, wk, wv);  // in flight while unit 0 is staged
   if (n > 0) stage(0, wk0, wv0);
+  DKV_TL(tl_mfma, 1);
   __syncthreads();
   if (n > 0) dequant(unit(0), 0, 0);
+  DKV_TL(tl_mfma, 2);
   if (n > 1) stage(1, wk, wv);
   if (n > 2) raw_load(a, unit(2), h, wk, wv);
   for (int i = 0; i < n; ++i) {
@@ -462,7 +471,9 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ par
       if (i + 3 < n) raw_load(a, unit(i + 3), h, wk, wv);
     }
     compute(unit(i), i & 1);
+    if (i == 0) DKV_TL(tl_mfma, 3);
   }
+  DKV_TL(tl_mfma, 4);
 
   // Merge the two key groups: group 1 parks (max, sum, O) in LDS (over the
   // staging buffers, once every wave is past its last unit), group 0 folds it
@@ -487,6 +498,7 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ par
     }
   }
   __syncthreads();
+  DKV_TL(tl_mfma, 5);
   if (kg == 0 && wave_on) {
 #pragma unroll
     for (int nb = 0; nb < NBW; ++nb) {
@@ -554,6 +566,7 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, float* __restrict__ par
       }
     }
   }
+  DKV_TL(tl_mfma, 6);
 }
 
 template <int PREC>
@@ -563,11 +576,14 @@ static void launch_prec(const dkv_attn_args& a, const Plan& p, float* part_o, fl
   const int rows = R < MFMA_ROWS ? R : MFMA_ROWS;  // rows of the fullest row group
   const int nbw = ((rows + 15) / 16 + 3) / 4;       // blocks of the busiest wave
   if (nbw >= 3)
-    hipLaunchKernelGGL((attn_mfma_kernel<PREC, 3>), grid, dim3(MF_THREADS), 0, s, a, p.units, p.splits, part_o, part_ml);
+    hipLaunchKernelGGL((attn_mfma_kernel<PREC, 3>), grid, dim3(MF_THREADS), 0, s, a, p.units, p.splits, p.cap, part_o,
+                       part_ml);
   else if (nbw == 2)
-    hipLaunchKernelGGL((attn_mfma_kernel<PREC, 2>), grid, dim3(MF_THREADS), 0, s, a, p.units, p.splits, part_o, part_ml);
+    hipLaunchKernelGGL((attn_mfma_kernel<PREC, 2>), grid, dim3(MF_THREADS), 0, s, a, p.units, p.splits, p.cap, part_o,
+                       part_ml);
   else
-    hipLaunchKernelGGL((attn_mfma_kernel<PREC, 1>), grid, dim3(MF_THREADS), 0, s, a, p.units, p.splits, part_o, part_ml);
+    hipLaunchKernelGGL((attn_mfma_kernel<PREC, 1>), grid, dim3(MF_THREADS), 0, s, a, p.units, p.splits, p.cap, part_o,
+                       part_ml);
 }
 
 int launch_attn_mfma(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml, hipStream_t s) {
@@ -577,3 +593,11 @@ int launch_attn_mfma(const dkv_attn_args& a, const Plan& p, float* part_o, float
 }
 
 }  // namespace dkv
+
+#ifdef DKV_TIMELINE
+// Timeline build only: copies the frame-chunk kernel's stamps of the last launch.
+extern "C" int dkv_timeline_mfma(void* host, int64_t bytes) {
+  const int64_t n = sizeof(dkv::tl_mfma) < (uint64_t)bytes ? sizeof(dkv::tl_mfma) : bytes;
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(dkv::tl_mfma), n, 0, hipMemcpyDeviceToHost);
+}
+#endif

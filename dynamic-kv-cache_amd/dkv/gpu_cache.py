@@ -810,6 +810,7 @@ class GraphSteps:
         a.n_tiles, a.past = self.tiles_bound, self.past_bound
         a.layer, a.layers, a.heads, a.q_heads, a.nq = 0, self.cache.layers, self.cache.heads, q_heads, self.chunk
         a.precision = PRECISIONS[self.cache.precision]
+        a.step = self.dev.data_ptr() + self.cache.layers * self.job_bytes  # launches sized for any history
         return _lib.load().dkv_attend_workspace_bytes(ctypes.byref(a))
 
 
