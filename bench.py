@@ -8,8 +8,10 @@ causal chunk over 1024/4096/8128-token mixed histories) in us/layer, GB/s and TF
 candidate scoring (4 continuations of 8-24 tokens over a 6144-token 4-bit / 8-bit
 history); and the reference CPU path timed on this host (the oracle restatement).
 
-Attention timings rotate over distinct per-layer histories whose total exceeds the
-256 MB Infinity Cache, so the history is read from HBM.
+Every timed workload streams at least twice the 256 MB Infinity Cache (MALL) of distinct
+memory per rotation (attention: as many distinct per-layer histories as that takes; pack:
+two copies of the volume, alternated), so the bytes come from HBM. The launch floor (a graph
+of tiny dependent kernels) is reported beside the attention numbers.
 """
 import argparse
 import json
@@ -24,6 +26,8 @@ sys.path.insert(0, REPO)
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 LAYERS, HEADS, Q_HEADS, TILE = 32, 5, 15, 64
+MALL_BYTES = 256 << 20
+ROTATION_BYTES = 2 * MALL_BYTES  # distinct bytes every timed rotation streams
 PIPELINE = int(os.environ.get('DKV_PIPELINE', '8'))  # frames per pipelined graph replay in the e2e run
 
 
@@ -34,7 +38,14 @@ def parse():
     p.add_argument('--warmup', type=int, default=20)
     p.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
     p.add_argument('--only', choices=['pack', 'seg', 'attn', 'cand', 'e2e', 'all'], default='all')
-    p.add_argument('--rotate', type=int, default=48, help='distinct layers attention rotates over')
+    p.add_argument('--rotate', type=int, default=48,
+                   help='least number of distinct layers attention rotates over (more when the layers '
+                        'hold less than 512 MB together)')
+    p.add_argument('--timeline', choices=['short', 'mfma'],
+                   help='instead of the benchmark: workgroup timelines of one attention launch of that kernel, '
+                        'from the timeline build (python dynamic-kv-cache_amd/dkv/_build.py --timeline)')
+    p.add_argument('--past', type=int, default=8128, help='--timeline: history tokens')
+    p.add_argument('--nq', type=int, default=0, help='--timeline: chunk tokens (default 1 short, 64 mfma)')
     return p.parse_args()
 
 
@@ -62,16 +73,32 @@ def time_launches(fn, steps, warmup):
     return start.elapsed_time(end) / steps  # ms per launch
 
 
+PACK_SOURCES = ('dynamic-kv-cache_amd/csrc/dkv_pack.hip', 'dynamic-kv-cache_amd/csrc/dkv_common.h')
+
+
+def pack_source_hash():
+    """sha256 over the sources the pack kernel is built from (the ones its counters depend on)."""
+    import hashlib
+    h = hashlib.sha256()
+    for rel in PACK_SOURCES:
+        with open(os.path.join(REPO, rel), 'rb') as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def pack_traffic():
     """HBM bytes per pack launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes, each
-    scaled by what the counter reads for a 256 MiB copy (profiles/pack_batch_kernel_pack_volume.md)."""
+    scaled by what the counter reads for a 256 MiB copy (profiles/pack_batch_kernel_pack_volume.md).
+    (None, reason) when the counters were taken on other kernel sources than the ones built here."""
     path = os.path.join(REPO, 'profiles', 'pack_batch_kernel_traffic.json')
     if not os.path.exists(path):
-        return None
+        return None, 'no counter record'
     t = json.load(open(path))
+    if t.get('source_sha16') != pack_source_hash():
+        return None, 'counter record is for other pack sources (re-measure)'
     fetch = t['fetch_kib'] * t['copy_bytes'] / t['copy_fetch_kib']
     write = t['write_kib'] * t['copy_bytes'] / t['copy_write_kib']
-    return int(fetch + write)
+    return int(fetch + write), 'rocprofv3 FETCH_SIZE + WRITE_SIZE, scaled by a 256 MiB copy'
 
 
 def pack_bytes(bits, layers=LAYERS, heads=HEADS, tile=TILE):
@@ -97,21 +124,39 @@ def graph_of(fn, reps):
 
 
 def bench_pack(steps, warmup, reps=10):
-    """One step = one launch packing the whole volume; timed as graph replays of `reps` launches."""
+    """One step = one launch packing the whole volume; timed as graph replays of `reps` launches that
+    alternate between two copies of the volume (inputs and arenas), 824 MB of distinct bytes."""
     import torch
     from dkv.gpu_cache import GPUCache
     from dkv.workloads import pack_volume
     vol = pack_volume(seed=0, layers=LAYERS, frames=96)
     dev = torch.device('cuda:0')
-    k, v = vol['k'].to(dev), vol['v'].to(dev)
-    cache = GPUCache(None, layers=LAYERS, heads=HEADS, max_tokens=96 * TILE)
-    batch = cache.append_batch(k, v, vol['bits'], [TILE] * 96)
-    graph = graph_of(batch.run, reps)
+    batches = []
+    for _ in range(2):
+        k, v = vol['k'].to(dev), vol['v'].to(dev)
+        cache = GPUCache(None, layers=LAYERS, heads=HEADS, max_tokens=96 * TILE)
+        batches.append(cache.append_batch(k, v, vol['bits'], [TILE] * 96))
+    state = {'i': 0}
+
+    def launch():
+        batches[state['i'] % 2].run()
+        state['i'] += 1
+    graph = graph_of(launch, reps)  # reps is even: each replay alternates the two volumes
     rounds = max(1, steps // reps)
     ms = time_launches(graph.replay, rounds, max(1, warmup // reps)) / reps
     read, write = pack_bytes(vol['bits'])
     gbs = (read + write) / (ms * 1e-3) / 1e9
-    return dict(ms=ms, gbs=gbs, read_bytes=read, write_bytes=write, bits=vol['bits'], steps=rounds * reps)
+    return dict(ms=ms, gbs=gbs, read_bytes=read, write_bytes=write, bits=vol['bits'], steps=rounds * reps,
+                rotation_bytes=2 * (read + write))
+
+
+def bench_launch_floor(reps=200, rounds=20):
+    """us per launch of a graph of `reps` dependent tiny kernels (a one-element add): the fixed cost
+    every kernel in a dependent chain pays on this box, whatever it does."""
+    import torch
+    x = torch.zeros(1, device='cuda:0')
+    graph = graph_of(lambda: x.add_(1.0), reps)
+    return time_launches(graph.replay, rounds, 2) / reps * 1e3
 
 
 def bench_segments(steps, warmup, reps=10):
@@ -150,9 +195,20 @@ def bench_copy(steps, nbytes=256 << 20, reps=10):
     return dict(ms=ms, gbs=2 * nbytes / (ms * 1e-3) / 1e9, bytes=nbytes)
 
 
+def history_bytes(bits, lengths):
+    return sum(HEADS * 2 * n * {4: 40, 8: 72, 16: 128}[b] for b, n in zip(bits, lengths))
+
+
+def rotation_layers(bits, lengths, least):
+    """Distinct layers a rotation needs so that their histories hold ROTATION_BYTES together."""
+    per = history_bytes(bits, lengths)
+    return max(least, -(-ROTATION_BYTES // per))
+
+
 def attention_setup(past, rotate, bits, nq=64, segments=None, seed=0, precision='bf16', path='auto', splits=0):
     """`rotate` layers, each with its own copy of one seeded history, and one graph that runs
-    the attention of every layer once (distinct histories, so the reads come from HBM)."""
+    the attention of every layer once (distinct histories, so the reads come from HBM). Returns
+    (replay, bytes per layer, kept objects); keep['rotate'] is the layer count."""
     import ctypes
     import torch
     from dkv import _lib
@@ -165,9 +221,10 @@ def attention_setup(past, rotate, bits, nq=64, segments=None, seed=0, precision=
     q = outlier_values((Q_HEADS, nq, 64), g, 0).to(dev)[None]
     kn = outlier_values((HEADS, nq, 64), g, 0).to(dev)[None]
     vn = outlier_values((HEADS, nq, 64), g, 0).to(dev)[None]
-    cache = GPUCache(None, layers=rotate, heads=HEADS, max_tokens=past + nq, precision=precision)
     tiles = (past + TILE - 1) // TILE
     lengths = [min(TILE, past - TILE * i) for i in range(tiles)]
+    rotate = rotation_layers(bits, lengths, rotate)
+    cache = GPUCache(None, layers=rotate, heads=HEADS, max_tokens=past + nq, precision=precision)
     cache.append_batch(hk[None].expand(rotate, -1, -1, -1).contiguous(),
                        hv[None].expand(rotate, -1, -1, -1).contiguous(), bits, lengths)
     cache.select(16)
@@ -197,9 +254,10 @@ def attention_setup(past, rotate, bits, nq=64, segments=None, seed=0, precision=
     with torch.cuda.graph(graph):
         launch_all()
     torch.cuda.synchronize()
-    hist_bytes = sum(HEADS * 2 * n * {4: 40, 8: 72, 16: 128}[b] for b, n in zip(bits, lengths))
+    hist_bytes = history_bytes(bits, lengths)
     chunk_bytes = (Q_HEADS * nq * 64 * 2) * 2 + HEADS * nq * 64 * 2 * 2  # q + out, k_new + v_new
-    keep = dict(cache=cache, keep=(hk, hv, q, kn, vn, out, ws, args), graph=graph)
+    keep = dict(cache=cache, keep=(hk, hv, q, kn, vn, out, ws, args), graph=graph, rotate=rotate,
+                rotation_bytes=rotate * hist_bytes)
     return graph.replay, hist_bytes + chunk_bytes, keep
 
 
@@ -213,10 +271,11 @@ def bench_attention(past, steps, warmup, rotate, precision='bf16'):
     from dkv.workloads import bit_schedule
     bits = bit_schedule(past, (past + TILE - 1) // TILE)
     replay, nbytes, keep = attention_setup(past, rotate, bits, seed=past, precision=precision)
-    ms = time_launches(replay, max(1, steps // 10), max(1, warmup // 10)) / rotate
+    ms = time_launches(replay, max(1, steps // 10), max(1, warmup // 10)) / keep['rotate']
     flops = attention_flops(past, [64])
+    rot = dict(rotation_layers=keep['rotate'], rotation_mb=round(keep['rotation_bytes'] / 1e6, 1))
     del keep
-    return dict(us_per_layer=ms * 1e3, gbs=nbytes / (ms * 1e-3) / 1e9, tflops=flops / (ms * 1e-3) / 1e12,
+    return dict(us_per_layer=ms * 1e3, **rot, gbs=nbytes / (ms * 1e-3) / 1e9, tflops=flops / (ms * 1e-3) / 1e12,
                 bytes=nbytes, flops=flops, mfma_frac=flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
                 hbm_frac=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, **attainable(nbytes, flops, ms))
 
@@ -233,10 +292,11 @@ def bench_decode(past, nq, steps, warmup, rotate, precision='bf16'):
     from dkv.workloads import bit_schedule
     bits = bit_schedule(past, (past + TILE - 1) // TILE)
     replay, nbytes, keep = attention_setup(past, rotate, bits, nq=nq, seed=past + nq, precision=precision)
-    ms = time_launches(replay, max(1, steps // 10), max(1, warmup // 10)) / rotate
+    ms = time_launches(replay, max(1, steps // 10), max(1, warmup // 10)) / keep['rotate']
     flops = attention_flops(past, [nq])
+    rot = dict(rotation_layers=keep['rotate'], rotation_mb=round(keep['rotation_bytes'] / 1e6, 1))
     del keep
-    return dict(us_per_layer=ms * 1e3, gbs=nbytes / (ms * 1e-3) / 1e9, bytes=nbytes,
+    return dict(us_per_layer=ms * 1e3, **rot, gbs=nbytes / (ms * 1e-3) / 1e9, bytes=nbytes,
                 hbm_frac=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, **attainable(nbytes, flops, ms))
 
 
@@ -249,10 +309,11 @@ def bench_candidates(bits, steps, warmup, rotate, precision='bf16'):
     past = 6144
     replay, nbytes, keep = attention_setup(past, rotate, [bits] * (past // TILE), nq=bounds[-1], segments=bounds,
                                            seed=bits, precision=precision)
-    ms = time_launches(replay, max(1, steps // 10), max(1, warmup // 10)) / rotate
+    ms = time_launches(replay, max(1, steps // 10), max(1, warmup // 10)) / keep['rotate']
     flops = attention_flops(past, lengths)
+    rot = dict(rotation_layers=keep['rotate'], rotation_mb=round(keep['rotation_bytes'] / 1e6, 1))
     del keep
-    return dict(us_per_batch=ms * 1e3, gbs=nbytes / (ms * 1e-3) / 1e9, tflops=flops / (ms * 1e-3) / 1e12,
+    return dict(us_per_batch=ms * 1e3, **rot, gbs=nbytes / (ms * 1e-3) / 1e9, tflops=flops / (ms * 1e-3) / 1e12,
                 bytes=nbytes, flops=flops, lengths=lengths, hbm_frac=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
                 mfma_frac=flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, **attainable(nbytes, flops, ms))
 
@@ -313,48 +374,142 @@ def bench_e2e(frame_counts=(16, 64, 96), reps=2):
     return out
 
 
-def cpu_baselines(target_s=8.0):
-    """The reference CPU path restated in torch on this host's cores (oracle; timed, not checked)."""
+TIMELINE_EVENTS = {
+    'short': ['entry', 'first descriptor', 'first K/V', 'units done', 'workgroup merge'],
+    'mfma': ['entry', 'unit 0 staged', 'unit 0 dequantized', 'unit 0 computed', 'all units', 'key-group merge',
+             'stores'],
+}
+
+
+def timeline(kind, past, nq, rotate):
+    """Workgroup timelines of the attention kernel `kind` from the timeline build: lane 0 of each
+    workgroup stamps wall_clock64() (100 MHz) at numbered points; after timed graph replays over the
+    rotation, the stamps of the last launch are read and each event's median / min / max over the
+    workgroups is printed relative to the earliest entry."""
+    import ctypes
+    import numpy as np
     import torch
-    from dkv.workloads import frame_chunk_case, pack_volume
-    from oracle.cpu_path import MixedPrecisionCache, cpu_attention_step
-    from oracle.kv_quantization import pack
-    cores = torch.get_num_threads()
-    # Pack: 2 layers of the pack workload (1/16 of the volume), every tile packed as the CPU path does.
-    vol = pack_volume(seed=0, layers=2, frames=96)
+    from dkv import _build, _lib
+    from dkv.workloads import bit_schedule
+    if not os.path.exists(_build.TIMELINE_LIB_PATH):
+        sys.exit(f'{_build.TIMELINE_LIB_PATH} is missing: python dynamic-kv-cache_amd/dkv/_build.py --timeline')
+    _build.LIB_PATH = _build.TIMELINE_LIB_PATH
+    lib = _lib.load()
+    fn = getattr(lib, 'dkv_timeline_' + kind)
+    fn.restype, fn.argtypes = ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64]
+    nq = nq or (1 if kind == 'short' else 64)
+    bits = bit_schedule(past, (past + TILE - 1) // TILE)
+    replay, nbytes, keep = attention_setup(past, rotate, bits, nq=nq, seed=past + nq, path=kind)
+    ms = time_launches(replay, 10, 2) / keep['rotate']
+    torch.cuda.synchronize()
+    stamps = np.zeros((1 << 14) * 8, dtype=np.uint64)
+    _lib.check(fn(stamps.ctypes.data, stamps.nbytes), 'dkv_timeline_' + kind)
+    t = stamps.reshape(-1, 8).astype(np.int64)
+    t = t[t[:, 0] > 0]
+    rel = (t - t[:, 0].min()) * 10 / 1000.0  # 100 MHz ticks -> us
+    print(f'# {kind} kernel, past={past} nq={nq}: {ms * 1e3:.2f} us/layer (timeline build), '
+          f'{len(t)} workgroups recorded', flush=True)
+    for e, name in enumerate(TIMELINE_EVENTS[kind]):
+        col = rel[:, e][t[:, e] > 0]
+        if len(col):
+            print(f'#   {name:20s} median {np.median(col):6.2f}  min {col.min():6.2f}  max {col.max():6.2f} us',
+                  flush=True)
+
+
+def cpu_model():
+    try:
+        for line in open('/proc/cpuinfo'):
+            if line.startswith('model name'):
+                return line.split(':', 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or 'unknown'
+
+
+def _timed(fn, seconds):
+    """Seconds per fn() call: repeated until `seconds` have passed (at least twice)."""
     t0 = time.perf_counter()
     reps = 0
-    while True:
+    while reps < 2 or time.perf_counter() - t0 < seconds:
+        fn()
+        reps += 1
+    return (time.perf_counter() - t0) / reps
+
+
+def cpu_baselines(leg_s=1.5):
+    """The reference CPU path restated in torch (oracle/cpu_path.py, src/cache_manager.py:43-63) on this
+    host's cores, at the affinity thread count and at 4 threads (the reference's setting,
+    configs/default.json:7). Legs, each a bounded sample of its workload:
+      pack      2 of the 32 layers of the pack workload (96 tiles, K and V), as the CPU path packs them
+      attn_8128 one layer's update + causal SDPA for a 64-token frame over 8128 mixed-width tokens
+      cfg0      the CPU-runnable plumbing case: 16 mixed-width 64-token tiles appended through
+                update() (each call dequantizes the history so far), then one 64-token frame's attention
+      cand_4, cand_8  4 candidates of 8-24 tokens, each on its own fork (the reference's candidate
+                protocol), over 6144 tokens of all-4-bit / all-8-bit history: ms per batch of 4."""
+    import torch
+    from dkv.workloads import bit_schedule, candidate_lengths, frame_chunk_case, outlier_values, pack_volume
+    from oracle.cpu_path import MixedPrecisionCache, cpu_attention_step
+    from oracle.kv_quantization import pack
+    affinity = len(os.sched_getaffinity(0))
+    share = int(os.environ.get('OMP_NUM_THREADS', '0') or 0)  # the process's CPU share where one is set
+    affinity = min(affinity, share) if share > 0 else affinity
+    vol = pack_volume(seed=0, layers=2, frames=96)
+    read, write = pack_bytes(vol['bits'], layers=2)
+
+    def pack_leg():
         for f, b in enumerate(vol['bits']):
             for layer in range(2):
                 pack(vol['k'][layer:layer + 1, :, 64 * f:64 * f + 64], b)
                 pack(vol['v'][layer:layer + 1, :, 64 * f:64 * f + 64], b)
-        reps += 1
-        if time.perf_counter() - t0 > target_s / 2:
-            break
-    dt = (time.perf_counter() - t0) / reps
-    read, write = pack_bytes(vol['bits'], layers=2)
-    pack_gbs = (read + write) / dt / 1e9
-    # Attention: the CPU path's per-layer update + SDPA for one 64-token frame over 8128 history tokens.
+
+    def history(bits, k, v):
+        c = MixedPrecisionCache()
+        for i, b in enumerate(bits):
+            c.select(b)
+            c.update(k[None, :, 64 * i:64 * i + 64], v[None, :, 64 * i:64 * i + 64], 0)
+        return c
+
+    def fork(c):
+        b = MixedPrecisionCache()
+        b.segments = {0: list(c.segments[0])}
+        b.select(16)
+        return b
+
     case = frame_chunk_case(8128, seed=8128)
-    c = MixedPrecisionCache()
-    for i, b in enumerate(case['bits']):
-        c.select(b)
-        c.update(case['k_hist'][None, :, 64 * i:64 * i + 64], case['v_hist'][None, :, 64 * i:64 * i + 64], 0)
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
-        c2 = MixedPrecisionCache()
-        c2.segments = {0: list(c.segments[0])}
-        c2.select(16)
-        cpu_attention_step(c2, case['q'][None], case['k_new'][None], case['v_new'][None])
-        reps += 1
-        if time.perf_counter() - t0 > target_s / 2:
-            break
-    attn_ms = (time.perf_counter() - t0) / reps * 1e3
-    return dict(pack_gbs=pack_gbs, attn_ms_per_layer_8128=attn_ms, cores=cores,
-                pack_sample='2 of 32 layers of the pack workload (96 tiles, K and V)',
-                attn_sample='one layer, 64-token frame over 8128 mixed history tokens (127 tiles)')
+    c8128 = history(case['bits'], case['k_hist'], case['v_hist'])
+    cfg0 = frame_chunk_case(1024, seed=1024)
+    g = torch.Generator().manual_seed(3)
+    lengths = candidate_lengths(0, 4)
+    cands = [tuple(outlier_values(shape, g, 0) for shape in ((Q_HEADS, n, 64), (HEADS, n, 64), (HEADS, n, 64)))
+             for n in lengths]
+    hist_kv = (outlier_values((HEADS, 6144, 64), g, 0), outlier_values((HEADS, 6144, 64), g, 0))
+    cand_hist = {b: history([b] * 96, *hist_kv) for b in (4, 8)}
+
+    def cfg0_leg():
+        c = history(cfg0['bits'], cfg0['k_hist'], cfg0['v_hist'])
+        c.select(16)
+        cpu_attention_step(c, cfg0['q'][None], cfg0['k_new'][None], cfg0['v_new'][None])
+
+    def cand_leg(b):
+        for q, k, v in cands:
+            cpu_attention_step(fork(cand_hist[b]), q[None], k[None], v[None])
+
+    out = {}
+    saved = torch.get_num_threads()
+    for threads in dict.fromkeys((affinity, 4)):
+        torch.set_num_threads(threads)
+        pack_s = _timed(pack_leg, leg_s)
+        out[str(threads)] = dict(
+            pack_gbs=round((read + write) / pack_s / 1e9, 4),
+            attn_8128_ms=round(_timed(lambda: cpu_attention_step(fork(c8128), case['q'][None], case['k_new'][None],
+                                                                  case['v_new'][None]), leg_s) * 1e3, 3),
+            cfg0_ms=round(_timed(cfg0_leg, leg_s) * 1e3, 3),
+            cand_4_ms=round(_timed(lambda: cand_leg(4), leg_s) * 1e3, 3),
+            cand_8_ms=round(_timed(lambda: cand_leg(8), leg_s) * 1e3, 3))
+    torch.set_num_threads(saved)
+    return dict(threads=out, cores=affinity, cpu_model=cpu_model(), candidate_lengths=lengths,
+                pack_sample='2 of 32 layers of the pack workload (96 tiles, K and V)')
 
 
 def main():
@@ -368,6 +523,9 @@ def main():
     if not torch.cuda.is_available():
         print(json.dumps(dict(error='no HIP device visible')), flush=True)
         sys.exit(2)
+    if args.timeline:
+        timeline(args.timeline, args.past, args.nq, args.rotate)
+        return
     from dkv import _lib
     _lib.load()
     res = {}
@@ -380,6 +538,9 @@ def main():
         r = res['segments'] = bench_segments(args.steps, args.warmup)
         print(f"# segments: export {r['export_us']:.1f} us ({r['export_gbs']:.0f} GB/s), import {r['import_us']:.1f} "
               f"us ({r['import_gbs']:.0f} GB/s), round trip equal {r['arena_round_trip_equal']}", flush=True)
+    if args.only in ('attn', 'cand', 'all'):
+        res['launch_floor_us'] = bench_launch_floor()
+        print(f"# launch floor: {res['launch_floor_us']:.2f} us per dependent launch in a graph", flush=True)
     if args.only in ('attn', 'all'):
         res['attention'] = {}
         for prec in ('bf16', 'fp32'):
@@ -418,10 +579,15 @@ def main():
                              'seeded 40/40/20 4/8/16-bit tiles, one launch', parallelism='none (1 GPU)'),
     )
     if p:
+        traffic, traffic_source = pack_traffic()
         line['roofline'] = dict(bound='hbm', achieved=round(p['gbs'], 1), peak=HBM_PEAK_GBS,
-                                unit='GB/s', frac=round(p['gbs'] / HBM_PEAK_GBS, 4), traffic=pack_traffic(),
-                                algorithmic_bytes=p['read_bytes'] + p['write_bytes'])
+                                unit='GB/s', frac=round(p['gbs'] / HBM_PEAK_GBS, 4), traffic=traffic,
+                                traffic_source=traffic_source,
+                                algorithmic_bytes=p['read_bytes'] + p['write_bytes'],
+                                rotation_bytes=p['rotation_bytes'])
         line['copy_reference_gbs'] = round(res['copy']['gbs'], 1)
+    if 'launch_floor_us' in res:
+        line['launch_floor_us'] = round(res['launch_floor_us'], 3)
     if 'attention' in res:
         line['attention'] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in r.items()}
                              for k, r in res['attention'].items()}
@@ -436,10 +602,14 @@ def main():
     if 'e2e' in res:
         line['e2e'] = res['e2e']
     if cpu:
-        line['cpu_baseline'] = dict(value=round(cpu['pack_gbs'], 4), unit='GB/s', cores=cpu['cores'], kind='port',
-                                    sample=cpu['pack_sample'],
-                                    attn_ms_per_layer_8128=round(cpu['attn_ms_per_layer_8128'], 3),
-                                    attn_sample=cpu['attn_sample'])
+        main_threads = str(cpu['cores'])
+        line['cpu_baseline'] = dict(
+            value=cpu['threads'][main_threads]['pack_gbs'], unit='GB/s', cores=cpu['cores'], kind='port',
+            sample=cpu['pack_sample'], cpu_model=cpu['cpu_model'], by_threads=cpu['threads'],
+            legs='pack_gbs: pack of 2 layers x 96 tiles; attn_8128_ms: one layer, 64-token frame over 8128 '
+                 'mixed tokens; cfg0_ms: 16 mixed tiles appended + one 64-token frame (1024-token plumbing '
+                 'case); cand_4_ms / cand_8_ms: 4 candidates (%s tokens) over 6144 all-4-bit / all-8-bit '
+                 'tokens' % '/'.join(map(str, cpu['candidate_lengths'])))
     print(json.dumps(line), flush=True)
 
 

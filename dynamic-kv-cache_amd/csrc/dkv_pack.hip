@@ -145,13 +145,15 @@ __device__ __forceinline__ void pack_loaded(const dkv_pack_job& j, int kv, int h
   const bool one_tile = rfirst / TILE == rlast / TILE;
   const RowDst d0 = row_dst(j, kv, head, tok0, arena, layers, heads);
   constexpr int RB = BITS == 4 ? 32 : (BITS == 8 ? 64 : 128);
+  // Arena stores are nontemporal: lines written with plain stores stay dirty in
+  // L2 and the end of the kernel writes all of them back before it completes.
   if (BITS == 16) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int r = 8 * i + (lane >> 3);
       if (r >= nrows) continue;
       uint8_t* dst = one_tile ? d0.payload + r * 128 : row_dst(j, kv, head, tok0 + r, arena, layers, heads).payload;
-      *reinterpret_cast<u32x4*>(dst + 16 * c) = w[i];
+      __builtin_nontemporal_store(w[i], reinterpret_cast<u32x4*>(dst + 16 * c));
     }
     return;
   }
@@ -198,7 +200,7 @@ __device__ __forceinline__ void pack_loaded(const dkv_pack_job& j, int kv, int h
     }
     return;
   }
-  if (valid) d0.meta[lane] = make_float2(a, s);
+  if (valid) __builtin_nontemporal_store((f32x2_t{a, s}), reinterpret_cast<f32x2_t*>(d0.meta + lane));
   // Packed rows back through LDS (the wave's own region, already read), then
   // contiguous 16-byte stores: RB bytes per row, rows back to back.
   wave_sync_lds();
@@ -211,7 +213,7 @@ __device__ __forceinline__ void pack_loaded(const dkv_pack_job& j, int kv, int h
   for (int i = 0; i < RB / 16; ++i) {
     const int off = 16 * (lane + 64 * i);
     if (off < bytes)
-      *reinterpret_cast<u32x4*>(d0.payload + off) = *reinterpret_cast<const u32x4*>(lds + off);
+      __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(lds + off), reinterpret_cast<u32x4*>(d0.payload + off));
   }
 }
 

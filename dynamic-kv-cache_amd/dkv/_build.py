@@ -21,6 +21,10 @@ CSRC = os.path.join(ROOT, 'csrc')
 INCLUDE = os.path.join(REPO, 'include')
 LIB_NAME = 'libdkv.so'
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
+# The timeline build (-DDKV_TIMELINE): the attention kernels also record per-workgroup
+# wall-clock stamps that dkv_timeline_short / dkv_timeline_mfma copy out. A diagnostic library,
+# never the one the package loads unless bench.py --timeline points it there.
+TIMELINE_LIB_PATH = os.path.join(PKG_DIR, 'libdkv_timeline.so')
 ARCH = os.environ.get('DKV_OFFLOAD_ARCH', 'gfx950')
 
 HIPCC_FLAGS = [
@@ -42,9 +46,10 @@ def hipcc():
     return path
 
 
-def build(verbose=False, extra=()):
-    """Compiles every csrc/*.hip into one shared library next to this file."""
-    tmp = LIB_PATH + '.tmp'
+def build(verbose=False, extra=(), out=None):
+    """Compiles every csrc/*.hip into one shared library next to this file (or at `out`)."""
+    out = out or LIB_PATH
+    tmp = out + '.tmp'
     cmd = [hipcc(), *HIPCC_FLAGS, *extra, '-I', INCLUDE, '-I', CSRC, '-o', tmp, *sources()]
     if verbose:
         print(' '.join(cmd), flush=True)
@@ -52,9 +57,12 @@ def build(verbose=False, extra=()):
     if proc.returncode != 0:
         sys.stderr.write(proc.stdout + proc.stderr)
         raise RuntimeError(f'hipcc failed with status {proc.returncode}')
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == '__main__':
-    print(build(verbose=True))
+    if '--timeline' in sys.argv[1:]:
+        print(build(verbose=True, extra=['-DDKV_TIMELINE'], out=TIMELINE_LIB_PATH))
+    else:
+        print(build(verbose=True))

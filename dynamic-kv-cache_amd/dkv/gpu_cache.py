@@ -482,7 +482,12 @@ class GPUCache(_CacheBase):
         return other
 
     def accounting(self):
-        """Used vs. allocated bytes with the reference's keys (src/gpu_cache.py:134-149)."""
+        """Used vs. allocated bytes with the reference's keys and formulas (src/gpu_cache.py:134-149).
+
+        token_mapping_bytes is the reference's 5 bytes per token (its int32 row index plus uint8
+        width code, src/gpu_cache.py:143), so gpu_cache_used_bytes compares with the reference's
+        figures; this cache maps tokens with one 16-byte descriptor per 64-token tile instead,
+        reported as tile_table_bytes."""
         allocated = self.arena.numel() + self.tiles.numel()
         used = {4: 0, 8: 0, 16: 0}
         n = self.seen[0]
@@ -490,14 +495,14 @@ class GPUCache(_CacheBase):
             used[bits] += max(0, min(n, end) - start)
         payload = self.layers * 2 * self.heads * self.dim * sum(used[b] * b / 8 for b in used)
         scales = self.layers * 2 * self.heads * 8 * (used[4] + used[8])
-        mapping = 16 * self._tiles_before(n)
+        mapping = 5 * n
         return dict(gpu_cache_used_bytes=int(payload + scales + mapping),
                     gpu_cache_allocated_bytes=allocated, cpu_cache_payload_bytes=0,
                     payload_bytes=int(payload), quantization_metadata_bytes=int(scales),
                     token_mapping_bytes=mapping, logical_index_capacity=self.capacity,
                     precision_pool_capacities=self.caps,
                     used_tokens=n, precision_token_counts=used,
-                    arena_used_bytes=self.arena_used)
+                    arena_used_bytes=self.arena_used, tile_table_bytes=16 * self._tiles_before(n))
 
 
     # -- HIP graph replays (no reference counterpart) ---------------------------

@@ -77,7 +77,9 @@ def test_accounting_reference_identities():
     assert a['gpu_cache_used_bytes'] == a['payload_bytes'] + a['quantization_metadata_bytes'] + a['token_mapping_bytes']
     assert a['precision_token_counts'] == {4: 64, 8: 64, 16: 64}
     assert a['gpu_cache_allocated_bytes'] >= a['arena_used_bytes']
-    assert a['used_tokens'] == 192 and a['token_mapping_bytes'] == 3 * 16
+    # the reference's 5 bytes per token (src/gpu_cache.py:143); the tile table is reported apart
+    assert a['used_tokens'] == 192 and a['token_mapping_bytes'] == 5 * 192
+    assert a['tile_table_bytes'] == 3 * 16
 
 
 def test_graph_step_jobs_encode_like_ctypes_pack_jobs():
