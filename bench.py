@@ -374,18 +374,19 @@ def bench_e2e(frame_counts=(16, 64, 96), reps=2):
     return out
 
 
-TIMELINE_EVENTS = {
-    'short': ['entry', 'first descriptor', 'first K/V', 'units done', 'workgroup merge'],
-    'mfma': ['entry', 'unit 0 staged', 'unit 0 dequantized', 'unit 0 computed', 'all units', 'key-group merge',
-             'stores'],
+TIMELINE_EVENTS = {  # stamp index -> name, in the order printed
+    'short': [(0, 'entry'), (5, 'arguments'), (1, 'first descriptor'), (2, 'first K/V'), (3, 'units done'),
+              (4, 'workgroup merge')],
+    'mfma': [(0, 'entry'), (7, 'arguments'), (1, 'unit 0 staged'), (2, 'unit 0 dequantized'),
+             (3, 'unit 0 computed'), (4, 'all units'), (5, 'key-group merge'), (6, 'stores')],
 }
 
 
 def timeline(kind, past, nq, rotate):
     """Workgroup timelines of the attention kernel `kind` from the timeline build: lane 0 of each
     workgroup stamps wall_clock64() (100 MHz) at numbered points; after timed graph replays over the
-    rotation, the stamps of the last launch are read and each event's median / min / max over the
-    workgroups is printed relative to the earliest entry."""
+    rotation, the stamps of the last launch (and of its split-merge kernel) are read and each
+    event's median / min / max over the workgroups is printed relative to the earliest entry."""
     import ctypes
     import numpy as np
     import torch
@@ -395,24 +396,31 @@ def timeline(kind, past, nq, rotate):
         sys.exit(f'{_build.TIMELINE_LIB_PATH} is missing: python dynamic-kv-cache_amd/dkv/_build.py --timeline')
     _build.LIB_PATH = _build.TIMELINE_LIB_PATH
     lib = _lib.load()
-    fn = getattr(lib, 'dkv_timeline_' + kind)
-    fn.restype, fn.argtypes = ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64]
     nq = nq or (1 if kind == 'short' else 64)
     bits = bit_schedule(past, (past + TILE - 1) // TILE)
     replay, nbytes, keep = attention_setup(past, rotate, bits, nq=nq, seed=past + nq, path=kind)
     ms = time_launches(replay, 10, 2) / keep['rotate']
     torch.cuda.synchronize()
-    stamps = np.zeros((1 << 14) * 8, dtype=np.uint64)
-    _lib.check(fn(stamps.ctypes.data, stamps.nbytes), 'dkv_timeline_' + kind)
-    t = stamps.reshape(-1, 8).astype(np.int64)
-    t = t[t[:, 0] > 0]
-    rel = (t - t[:, 0].min()) * 10 / 1000.0  # 100 MHz ticks -> us
+
+    def read(name):
+        f = getattr(lib, name)
+        f.restype, f.argtypes = ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64]
+        stamps = np.zeros((1 << 14) * 8, dtype=np.uint64)
+        _lib.check(f(stamps.ctypes.data, stamps.nbytes), name)
+        t = stamps.reshape(-1, 8).astype(np.int64)
+        return t[t[:, 0] > 0]
+    t = read('dkv_timeline_' + kind)
+    merge = read('dkv_timeline_combine')
+    t0 = t[:, 0].min()
     print(f'# {kind} kernel, past={past} nq={nq}: {ms * 1e3:.2f} us/layer (timeline build), '
-          f'{len(t)} workgroups recorded', flush=True)
-    for e, name in enumerate(TIMELINE_EVENTS[kind]):
-        col = rel[:, e][t[:, e] > 0]
+          f'{len(t)} workgroups recorded; merge kernel: {len(merge)} workgroups', flush=True)
+    events = [(t, e, name) for e, name in TIMELINE_EVENTS[kind]]
+    events += [(merge, e, 'merge ' + name) for e, name in enumerate(['entry', 'arguments', 'partials merged',
+                                                                   'row stored'])]
+    for tt, e, name in events:
+        col = (tt[:, e][tt[:, e] > 0] - t0) * 10 / 1000.0  # 100 MHz ticks -> us
         if len(col):
-            print(f'#   {name:20s} median {np.median(col):6.2f}  min {col.min():6.2f}  max {col.max():6.2f} us',
+            print(f'#   {name:22s} median {np.median(col):6.2f}  min {col.min():6.2f}  max {col.max():6.2f} us',
                   flush=True)
 
 

@@ -238,6 +238,11 @@ attn_vec_kernel(dkv_attn_args a, int units, int splits, int cap, float* __restri
 // Both merges read the partials once, with nontemporal loads (past 8128: 18.7 -> 18.5 us per
 // layer; candidate batches 15.9 -> 15.7 us).
 //
+#ifdef DKV_TIMELINE
+// events (both merge kernels): 0 entry, 1 arguments arrived, 2 partials merged, 3 row stored
+static __device__ uint64_t tl_comb[TL_SLOTS * TL_EVENTS];
+#endif
+//
 // Precision-1 merge (unnormalized fp32 O partials, 256 bytes per row): one
 // wave per query row. Lane l = 16 j + c reads 16-byte chunk c (columns
 // 4c + [0, 4)) of split s0 + 4 i + j for i = 0..15, so each load instruction
@@ -247,6 +252,7 @@ attn_vec_kernel(dkv_attn_args a, int units, int splits, int cap, float* __restri
 __global__ void __launch_bounds__(256)
 combine_kernel(dkv_attn_args a, int splits, int cap, int short_plan, const float* __restrict__ part_o,
                const float2* __restrict__ part_ml) {
+  DKV_TL(tl_comb, 0);
   const int h = blockIdx.y;
   const int G = a.q_heads / a.heads;
   const int R = G * a.nq;
@@ -258,6 +264,7 @@ combine_kernel(dkv_attn_args a, int splits, int cap, int short_plan, const float
   // partials written (graph replays: fewer), by the producing kernel's rule
   const int active = short_plan ? short_runtime_plan(a, hs, units, splits) : runtime_plan(a, hs, units, splits, cap);
   if (active <= 1) return;  // one split ran and stored the output itself
+  DKV_TL(tl_comb, 1);
   const int64_t base = (int64_t)h * splits * R + r;
   const int j = lane >> 4, c = lane & 15;
   const float4* rows = reinterpret_cast<const float4*>(part_o);  // 16 chunks of 16 bytes per row
@@ -299,6 +306,7 @@ combine_kernel(dkv_attn_args a, int splits, int cap, int short_plan, const float
   for (int o = 16; o < 64; o <<= 1)
 #pragma unroll
     for (int e = 0; e < 4; ++e) acc[e] += __shfl_xor(acc[e], o);
+  DKV_TL(tl_comb, 2);
   if (j != 0) return;
   const float inv = 1.f / L;
   const float v0 = acc[0] * inv, v1 = acc[1] * inv, v2 = acc[2] * inv, v3 = acc[3] * inv;
@@ -309,6 +317,7 @@ combine_kernel(dkv_attn_args a, int splits, int cap, int short_plan, const float
   else
     *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + off) =
         make_uint2(f32_to_bf16_rne(v0) | (f32_to_bf16_rne(v1) << 16), f32_to_bf16_rne(v2) | (f32_to_bf16_rne(v3) << 16));
+  DKV_TL(tl_comb, 3);
 }
 
 // Precision-0 merge (fp16 O / sum partials, 128 bytes per row in half_slot()
@@ -320,6 +329,7 @@ combine_kernel(dkv_attn_args a, int splits, int cap, int short_plan, const float
 __global__ void __launch_bounds__(256)
 combine_half_kernel(dkv_attn_args a, int splits, int cap, int short_plan, const float* __restrict__ part_o,
                     const float2* __restrict__ part_ml) {
+  DKV_TL(tl_comb, 0);
   const int h = blockIdx.y;
   const int G = a.q_heads / a.heads;
   const int R = G * a.nq;
@@ -331,6 +341,7 @@ combine_half_kernel(dkv_attn_args a, int splits, int cap, int short_plan, const 
   // partials written (graph replays: fewer), by the producing kernel's rule
   const int active = short_plan ? short_runtime_plan(a, hs, units, splits) : runtime_plan(a, hs, units, splits, cap);
   if (active <= 1) return;  // one split ran and stored the output itself
+  DKV_TL(tl_comb, 1);
   const int64_t base = (int64_t)h * splits * R + r;
   const int j = lane >> 3, c = lane & 7;
   const uint4* rows = reinterpret_cast<const uint4*>(part_o);  // 8 chunks of 16 bytes per row
@@ -380,6 +391,7 @@ combine_half_kernel(dkv_attn_args a, int splits, int cap, int short_plan, const 
   for (int o = 8; o < 64; o <<= 1)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], o);
+  DKV_TL(tl_comb, 2);
   if (j != 0) return;
   const float inv = 1.f / L;
   const int gq = r / a.nq, m = r - gq * a.nq;
@@ -395,6 +407,7 @@ combine_half_kernel(dkv_attn_args a, int splits, int cap, int short_plan, const 
       *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + off + col) =
           make_uint2(f32_to_bf16_rne(v0) | (f32_to_bf16_rne(v1) << 16), f32_to_bf16_rne(v2) | (f32_to_bf16_rne(v3) << 16));
   }
+  DKV_TL(tl_comb, 3);
 }
 
 // ---------------------------------------------------------------------------
@@ -632,3 +645,11 @@ int dkv_attend_noalloc(const dkv_attn_args* args, void* stream) {
 }
 
 }  // extern "C"
+
+#ifdef DKV_TIMELINE
+// Timeline build only: copies the merge kernels' stamps of the last launch.
+extern "C" int dkv_timeline_combine(void* host, int64_t bytes) {
+  const int64_t n = sizeof(dkv::tl_comb) < (uint64_t)bytes ? sizeof(dkv::tl_comb) : bytes;
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(dkv::tl_comb), n, 0, hipMemcpyDeviceToHost);
+}
+#endif

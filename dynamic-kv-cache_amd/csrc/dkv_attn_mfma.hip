@@ -183,7 +183,7 @@ __device__ __forceinline__ Unit unit_at(const dkv_attn_args& a, const Hist& hs, 
 // store only real rows.
 #ifdef DKV_TIMELINE
 // events: 0 entry, 1 first unit staged in LDS, 2 first unit dequantized, 3 first unit computed,
-// 4 last unit computed, 5 key groups merged, 6 stores issued
+// 4 last unit computed, 5 key groups merged, 6 stores issued, 7 arguments arrived
 static __device__ uint64_t tl_mfma[TL_SLOTS * TL_EVENTS];
 #endif
 
@@ -214,6 +214,7 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, int cap, float* __restr
   const int kg = wave >> 2, w = wave & 3;  // key group, wave within the group
   const int col = lane & 15, g = lane >> 4;
   if (split >= active) return;  // graph replay over a shorter history than the launch bound
+  DKV_TL(tl_mfma, 7);           // the argument block (and any step pair) has arrived
   const int u0 = (int)((int64_t)units * split / active);
   const int u1 = (int)((int64_t)units * (split + 1) / active);
   const float xs = a.scale * LOG2E;

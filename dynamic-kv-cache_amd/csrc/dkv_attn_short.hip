@@ -170,7 +170,7 @@ __device__ __forceinline__ Unit unit_of(const dkv_attn_args& a, const Hist& hs, 
 
 #ifdef DKV_TIMELINE
 // events: 0 entry, 1 first tile descriptor, 2 first unit's K/V bytes, 3 units done,
-// 4 workgroup merge
+// 4 workgroup merge, 5 arguments arrived
 static __device__ uint64_t tl_short[TL_SLOTS * TL_EVENTS];
 #endif
 
@@ -187,6 +187,7 @@ attn_short_kernel(dkv_attn_args a, int units, int nwg, float* __restrict__ part_
   const int active = short_runtime_plan(a, hs, units, nwg);
   const int wg = blockIdx.x, h = blockIdx.y;
   if (wg >= active) return;  // graph replay over a shorter history than the launch bound
+  DKV_TL(tl_short, 5);       // the argument block (and any step pair) has arrived
   const int G = a.q_heads / a.heads;
   const int R = G * a.nq;  // <= 16 (checked on the host)
   const int t = threadIdx.x, lane = t & 63;
