@@ -783,6 +783,11 @@ class GraphSteps:
         k, v = c._kv_view(k), c._kv_view(v)
         self.kv[layer] = (k, v)
         self.kv_version += 1
+        if not torch.cuda.is_current_stream_capturing():
+            # an eager launch reads its job when it runs: upload the job again so that it carries
+            # the K/V views just recorded (the last upload may predate them: null sources), ordered
+            # on this stream before the launch
+            self.upload()
         _lib.check(_lib.load().dkv_pack_batch(self.dev.data_ptr() + layer * self.job_bytes, 1, self.chunk,
                                               c.arena.data_ptr(), c.arena_bytes, c.tiles.data_ptr(), c.layers,
                                               c.heads, _lib.stream_handle(c.device)), 'dkv_pack_batch')

@@ -39,6 +39,9 @@ int main(void) {
   printf("dkv_pack_job size %zu\n", sizeof(dkv_pack_job));
   printf("dkv_attn_args size %zu\n", sizeof(dkv_attn_args));
   printf("dkv_segment_io size %zu\n", sizeof(dkv_segment_io));
+  printf("DKV_MAX_CHUNK_SEGS const %d\n", DKV_MAX_CHUNK_SEGS);
+  printf("DKV_NOALLOC_SCRATCH_BYTES const %d\n", DKV_NOALLOC_SCRATCH_BYTES);
+  printf("DKV_ABI_VERSION const %d\n", DKV_ABI_VERSION);
   %FIELDS%
   return 0;
 }
@@ -56,6 +59,9 @@ def test_struct_layout_matches_header(tmp_path, cls, cname):
     lines = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split('\n')
     sizes = {l.split()[0]: int(l.split()[2]) for l in lines if ' size ' in l}
     assert sizes[cname] == ctypes.sizeof(cls)
+    consts = {l.split()[0]: int(l.split()[2]) for l in lines if ' const ' in l}
+    assert consts == dict(DKV_MAX_CHUNK_SEGS=_lib.DKV_MAX_CHUNK_SEGS,
+                          DKV_NOALLOC_SCRATCH_BYTES=_lib.DKV_NOALLOC_SCRATCH_BYTES, DKV_ABI_VERSION=_lib.ABI_VERSION)
     for line in lines:
         parts = line.split()
         if len(parts) == 3 and parts[0] == cname and parts[1] != 'size':

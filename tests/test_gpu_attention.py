@@ -443,9 +443,11 @@ def test_short_chunk_rejects_too_many_rows(cuda):
 
 @pytest.mark.parametrize('precision', ['fp32', 'bf16'])
 def test_decode_steps_replayed_from_a_graph(cuda, precision):
-    """One-token decode steps recorded once in a HIP graph (the launch sized for the cache's
-    capacity, the history read from the device step pair) and replayed as the history grows from 0
-    to 9 tiles: every replay must equal a direct call on the same history bit for bit."""
+    """One-token decode steps (pack the token, attend over the history before it) recorded once in
+    a HIP graph (the launches sized for the cache's capacity, the history read from the device step
+    pair) and replayed as the history grows from 0 to 9 tiles: every replay's attention must equal a
+    direct call on the same history bit for bit (the direct call passes the tile descriptors by
+    value, the replay reads the device table the replays' packs wrote)."""
     announce(f'attention decode steps graph replay precision={precision}')
     torch.manual_seed(5)
     heads, q_heads = 5, 15
@@ -458,10 +460,12 @@ def test_decode_steps_replayed_from_a_graph(cuda, precision):
     c.graph_step()
     side = torch.cuda.Stream()
     with torch.cuda.stream(side):
+        c.append(kn, vn, 0)
         c.attend(q, kn, vn, 0, 0)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.cuda.graph(graph):  # a decode step: pack the token, then attend over the history before it
+        c.append(kn, vn, 0)
         out = c.attend(q, kn, vn, 0, 0)
     c.end_graph_steps()
     c.reset()
