@@ -435,28 +435,31 @@ def cpu_model():
     return platform.processor() or 'unknown'
 
 
-def _timed(fn, seconds):
-    """Seconds per fn() call: repeated until `seconds` have passed (at least twice)."""
-    t0 = time.perf_counter()
-    reps = 0
-    while reps < 2 or time.perf_counter() - t0 < seconds:
+def _timed(fn, reps=10):
+    """Median seconds per fn() call over `reps` calls after one untimed call."""
+    fn()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
         fn()
-        reps += 1
-    return (time.perf_counter() - t0) / reps
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2]
 
 
-def cpu_baselines(leg_s=1.5):
+def cpu_baselines(reps=10):
     """The reference CPU path restated in torch (oracle/cpu_path.py, src/cache_manager.py:43-63) on this
     host's cores, at the affinity thread count and at 4 threads (the reference's setting,
-    configs/default.json:7). Legs, each a bounded sample of its workload:
+    configs/default.json:7). Each leg is the median of `reps` calls after one untimed call, on a
+    bounded sample of its workload:
       pack      2 of the 32 layers of the pack workload (96 tiles, K and V), as the CPU path packs them
-      attn_8128 one layer's update + causal SDPA for a 64-token frame over 8128 mixed-width tokens
+      attn_P    one layer's update + causal SDPA for a 64-token frame over P = 1024 / 4096 / 8128
+                mixed-width tokens (the update dequantizes the whole history)
       cfg0      the CPU-runnable plumbing case: 16 mixed-width 64-token tiles appended through
                 update() (each call dequantizes the history so far), then one 64-token frame's attention
       cand_4, cand_8  4 candidates of 8-24 tokens, each on its own fork (the reference's candidate
                 protocol), over 6144 tokens of all-4-bit / all-8-bit history: ms per batch of 4."""
     import torch
-    from dkv.workloads import bit_schedule, candidate_lengths, frame_chunk_case, outlier_values, pack_volume
+    from dkv.workloads import candidate_lengths, frame_chunk_case, outlier_values, pack_volume
     from oracle.cpu_path import MixedPrecisionCache, cpu_attention_step
     from oracle.kv_quantization import pack
     affinity = len(os.sched_getaffinity(0))
@@ -484,8 +487,10 @@ def cpu_baselines(leg_s=1.5):
         b.select(16)
         return b
 
-    case = frame_chunk_case(8128, seed=8128)
-    c8128 = history(case['bits'], case['k_hist'], case['v_hist'])
+    frames = {}
+    for past in (1024, 4096, 8128):
+        case = frame_chunk_case(past, seed=past)
+        frames[past] = (case, history(case['bits'], case['k_hist'], case['v_hist']))
     cfg0 = frame_chunk_case(1024, seed=1024)
     g = torch.Generator().manual_seed(3)
     lengths = candidate_lengths(0, 4)
@@ -503,18 +508,21 @@ def cpu_baselines(leg_s=1.5):
         for q, k, v in cands:
             cpu_attention_step(fork(cand_hist[b]), q[None], k[None], v[None])
 
+    def frame_leg(past):
+        case, c = frames[past]
+        cpu_attention_step(fork(c), case['q'][None], case['k_new'][None], case['v_new'][None])
+
     out = {}
     saved = torch.get_num_threads()
     for threads in dict.fromkeys((affinity, 4)):
         torch.set_num_threads(threads)
-        pack_s = _timed(pack_leg, leg_s)
-        out[str(threads)] = dict(
-            pack_gbs=round((read + write) / pack_s / 1e9, 4),
-            attn_8128_ms=round(_timed(lambda: cpu_attention_step(fork(c8128), case['q'][None], case['k_new'][None],
-                                                                  case['v_new'][None]), leg_s) * 1e3, 3),
-            cfg0_ms=round(_timed(cfg0_leg, leg_s) * 1e3, 3),
-            cand_4_ms=round(_timed(lambda: cand_leg(4), leg_s) * 1e3, 3),
-            cand_8_ms=round(_timed(lambda: cand_leg(8), leg_s) * 1e3, 3))
+        r = dict(pack_gbs=round((read + write) / _timed(pack_leg, reps) / 1e9, 4))
+        for past in frames:
+            r[f'attn_{past}_ms'] = round(_timed(lambda: frame_leg(past), reps) * 1e3, 3)
+        r['cfg0_ms'] = round(_timed(cfg0_leg, reps) * 1e3, 3)
+        r['cand_4_ms'] = round(_timed(lambda: cand_leg(4), reps) * 1e3, 3)
+        r['cand_8_ms'] = round(_timed(lambda: cand_leg(8), reps) * 1e3, 3)
+        out[str(threads)] = r
     torch.set_num_threads(saved)
     return dict(threads=out, cores=affinity, cpu_model=cpu_model(), candidate_lengths=lengths,
                 pack_sample='2 of 32 layers of the pack workload (96 tiles, K and V)')
@@ -614,10 +622,10 @@ def main():
         line['cpu_baseline'] = dict(
             value=cpu['threads'][main_threads]['pack_gbs'], unit='GB/s', cores=cpu['cores'], kind='port',
             sample=cpu['pack_sample'], cpu_model=cpu['cpu_model'], by_threads=cpu['threads'],
-            legs='pack_gbs: pack of 2 layers x 96 tiles; attn_8128_ms: one layer, 64-token frame over 8128 '
-                 'mixed tokens; cfg0_ms: 16 mixed tiles appended + one 64-token frame (1024-token plumbing '
-                 'case); cand_4_ms / cand_8_ms: 4 candidates (%s tokens) over 6144 all-4-bit / all-8-bit '
-                 'tokens' % '/'.join(map(str, cpu['candidate_lengths'])))
+            legs='median of 10 calls each; pack_gbs: pack of 2 layers x 96 tiles; attn_P_ms: one layer, '
+                 '64-token frame over P mixed tokens; cfg0_ms: 16 mixed tiles appended + one 64-token frame '
+                 '(1024-token plumbing case); cand_4_ms / cand_8_ms: 4 candidates (%s tokens) over 6144 '
+                 'all-4-bit / all-8-bit tokens' % '/'.join(map(str, cpu['candidate_lengths'])))
     print(json.dumps(line), flush=True)
 
 
