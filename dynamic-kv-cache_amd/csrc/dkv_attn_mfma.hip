@@ -14,10 +14,13 @@
 // Per unit:
 //   1. the raw K and V sub-blocks (codes + (offset, scale) pairs, or bf16 rows)
 //      are copied to LDS with one 16-byte load per thread each;
-//   2. the 512 threads dequantize (q*s + a as one fused multiply-add; the
-//      reference's Triton expression, src/gpu_kernels.py:67-68, is open to the
-//      same contraction under Triton's default fp fusion) into a bf16 K tile
-//      [key][d] and a transposed bf16 V tile [d][key];
+//   2. the 512 threads dequantize (q*s + a with a separately rounded multiply
+//      and add, the reference's unpack, src/kv_quantization.py:90-91, so K and
+//      V equal what reconstruct() returns) into a bf16 K tile [key][d] and a
+//      transposed bf16 V tile [d][key]. (A fused multiply-add, which a compiler
+//      may make of the Triton expression at src/gpu_kernels.py:67-68, rounds
+//      about 0.1% of the elements to another bf16 value; with logits near 65 one
+//      such K element of a dominant key moves an output by ~0.1.)
 //   3. each wave computes S^T = K Q^T for its blocks (keys on the MFMA M axis,
 //      queries on N), runs the online softmax per query column in registers,
 //      and accumulates O^T = V^T P^T with P^T taken straight from the S^T
@@ -102,7 +105,7 @@ constexpr float rescale_log2() { return PREC ? 8.f : 0.f; }
 __device__ __forceinline__ int padded(int off) { return off + ((off >> 7) << 4); }
 
 // 8 fp32 values q*s + a of row r, columns [8*db, 8*db + 8), of a 4/8-bit raw
-// sub-block in LDS (one fused multiply-add, the more accurate of the two roundings).
+// sub-block in LDS (multiply and add rounded separately, as the reference's unpack).
 __device__ __forceinline__ void dequant8(const uint8_t* raw, int bits, int rows, int r, int db, float* x) {
   const float2 as = *reinterpret_cast<const float2*>(raw + padded(rows * (int)row_bytes(bits) + 8 * r));
   float q[8];
@@ -123,7 +126,7 @@ __device__ __forceinline__ void dequant8(const uint8_t* raw, int bits, int rows,
     }
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) x[i] = __fmaf_rn(q[i], as.y, as.x);
+  for (int i = 0; i < 8; ++i) x[i] = __fadd_rn(__fmul_rn(q[i], as.y), as.x);
 }
 
 // Row r, columns [8*db, 8*db + 8), of a bf16 raw sub-block (16-bit tiles and chunk pieces).

@@ -112,8 +112,9 @@ __device__ __forceinline__ void load16(const dkv_attn_args& a, const Unit& un, i
 }
 
 // 16 values of a loaded row slice as fp32, zeros when `ok` is false (a row
-// past `valid`): codes * s + a (one fused multiply-add, as the frame-chunk
-// kernel dequantizes) for 4/8-bit, the bf16 values for 16-bit.
+// past `valid`): codes * s + a (multiply and add rounded separately, as the
+// reference's unpack and every other kernel here) for 4/8-bit, the bf16 values
+// for 16-bit.
 __device__ __forceinline__ void dequant16(const uint4& w0, const uint4& w1, float2 as, bool ok, int bits, int e0,
                                           float* x) {
   if (bits == 16) {
@@ -146,7 +147,7 @@ __device__ __forceinline__ void dequant16(const uint4& w0, const uint4& w1, floa
     for (int t = 0; t < 16; ++t) q[t] = (float)((u[t >> 2] >> (8 * (t & 3))) & 255u);
   }
 #pragma unroll
-  for (int t = 0; t < 16; ++t) x[t] = ok ? __fmaf_rn(q[t], as.y, as.x) : 0.f;
+  for (int t = 0; t < 16; ++t) x[t] = ok ? __fadd_rn(__fmul_rn(q[t], as.y), as.x) : 0.f;
 }
 
 // Unit u of KV head h (as get_unit), with the history tile's 16-byte

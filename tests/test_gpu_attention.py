@@ -372,6 +372,29 @@ def test_random_shapes_against_the_oracles(cuda, i, heads, group, nq, past, segm
         assert err <= max(2e-2, noise), (err, noise)
 
 
+@pytest.mark.parametrize('nq,paths', [(8, ('mfma', 'vector', 'auto')), (5, ('short', 'mfma', 'vector'))])
+def test_ill_conditioned_rows_dequantize_like_unpack(cuda, nq, paths):
+    """Rows whose softmax is dominated by two keys with logits near 65 (4 KV heads, GQA 3, a chunk over
+    4000 mixed tokens, seed 1039, found by a randomized sweep): one K element rounded to a neighbouring
+    bf16 value moves such a row by ~0.1. Every kernel therefore dequantizes exactly as the reference's
+    unpack, with a separately rounded multiply and add (src/kv_quantization.py:90-91), the form the
+    emulated reference kernel uses; a fused multiply-add rounds about 0.1% of K/V elements to another
+    bf16 value and put this case 0.107 away from it."""
+    announce(f'attention ill-conditioned rows nq={nq}')
+    case = frame_chunk_case(4000, seed=1039, heads=4, q_heads=12, nq=nq)
+    c, dk, dv = build(case, cuda)
+    ref = semantics_out(case, dk, dv, None, torch.float32)
+    tol = max(2e-2, reference_noise(case, dk, dv))
+    for path in paths:
+        for splits in (1, 0):
+            c, _, _ = build(case, cuda)
+            got = run(c, case, cuda, torch.float32, path=path, splits=splits, precision='bf16')
+            err = (got - ref).abs().max().item()
+            print(f'[bf16-vs-reference] ill-conditioned nq={nq} path={path} splits={splits}: max-abs {err:.4e} '
+                  f'(bound {tol:.4e})', flush=True)
+            assert err <= tol, (path, splits, err, tol)
+
+
 # -- the short-chunk kernel (decode steps: q_heads / heads * nq <= 16) ---------------------------
 @pytest.mark.parametrize('precision', ['fp32', 'bf16'])
 @pytest.mark.parametrize('past,nq', [(0, 1), (1, 1), (63, 4), (64, 5), (700, 1), (1000, 3), (8128, 1), (8128, 4)])
