@@ -157,7 +157,7 @@ __device__ __forceinline__ int short_runtime_plan(const dkv_attn_args& a, Hist& 
   const int want = a.splits > 0 ? min(a.splits, units) : (units + SHORT_UNITS - 1) / SHORT_UNITS;
   return max(1, min(nwg, want));
 }
-constexpr int MFMA_ROWS = 192;  // query rows per MFMA-path workgroup (4 waves x 3 x 16)
+constexpr int MFMA_ROWS = 192;  // query rows per MFMA-path workgroup (6 waves x 2 blocks x 16)
 
 // Precision-0 split partials hold O / sum in fp16, 64 values per row (128
 // bytes) in the order the MFMA kernel's lanes store them: the lane of 16-byte

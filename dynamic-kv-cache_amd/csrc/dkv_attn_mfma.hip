@@ -3,13 +3,15 @@
 // chunk times 3 GQA heads gives 192 query rows per KV head; a one-token decode
 // step fills 3 of the 16 rows of one block.
 //
-// Workgroup = 8 waves = one KV head, up to 192 query rows (every GQA head of
+// Workgroup = 12 waves = one KV head, up to 192 query rows (every GQA head of
 // that KV head), one contiguous range of units (64-key history tiles, then
 // 64-row pieces of the chunk). The waves form two key groups: group c
-// (waves 4c..4c+3) handles keys [32c, 32c + 32) of every unit, so two waves
-// share each SIMD and one's softmax overlaps the other's MFMAs. Wave w of a
-// group owns 16-row query blocks w, w+4, w+8. The two groups keep separate
-// online-softmax states and merge through LDS after the last unit.
+// (waves 6c..6c+5) handles keys [32c, 32c + 32) of every unit, so three waves
+// share each SIMD and one's softmax overlaps another's MFMAs. Wave w of a
+// group owns 16-row query blocks w and w+6 (at most 2 per wave, which keeps a
+// wave within the 168 VGPRs of 3 waves per SIMD). The two groups keep
+// separate online-softmax states and merge through LDS after the last unit.
+// Threads 0..511 stage and dequantize the units; the others only compute.
 //
 // Per unit:
 //   1. the raw K and V sub-blocks (codes + (offset, scale) pairs, or bf16 rows)
@@ -57,7 +59,9 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int MF_THREADS = 512;
+constexpr int KG_WAVES = 6;                // waves per key group
+constexpr int MF_THREADS = 2 * KG_WAVES * 64;  // 768
+constexpr int MF_LOADERS = 512;            // threads that load, stage and dequantize a unit
 constexpr int KS = 72;       // LDS row stride, in bf16 elements, of the K and V^T tiles
 constexpr int RAWP = 9216;   // padded raw bytes of one sub-block (64 rows x 128 B + 16 B per 128 B)
 constexpr int MRG_STRIDE = D + 4;  // fp32 row stride of the key-group merge: 16 query rows of one
@@ -134,7 +138,8 @@ __device__ __forceinline__ uint4 bf16_row8(const uint8_t* raw, int r, int db) {
   return *reinterpret_cast<const uint4*>(raw + padded(r * 128 + db * 16));
 }
 
-// One 16-byte piece of K (threads 0..511 -> pieces 0..511) and one of V.
+// One 16-byte piece of K (threads 0..511 -> pieces 0..511) and one of V;
+// threads 512 and up load nothing (every sub-block is at most 512 pieces).
 __device__ __forceinline__ void raw_load(const dkv_attn_args& a, const Unit& un, int h, uint4& wk, uint4& wv) {
   const int p = threadIdx.x;
   wk = wv = make_uint4(0, 0, 0, 0);
@@ -180,7 +185,7 @@ __device__ __forceinline__ Unit unit_at(const dkv_attn_args& a, const Hist& hs, 
   return un;
 }
 
-// NBW = 16-row query blocks each wave computes (1..3). A wave whose first
+// NBW = 16-row query blocks each wave computes (1..2). A wave whose first
 // block is past the last row skips the MFMA work (a scalar branch); other
 // waves compute all NBW blocks, those past the last row on zero queries, and
 // store only real rows.
@@ -214,7 +219,7 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, int cap, float* __restr
   const int R = G * a.nq;
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int kg = wave >> 2, w = wave & 3;  // key group, wave within the group
+  const int kg = wave / KG_WAVES, w = wave - kg * KG_WAVES;  // key group, wave within the group
   const int col = lane & 15, g = lane >> 4;
   if (split >= active) return;  // graph replay over a shorter history than the launch bound
   DKV_TL(tl_mfma, 7);           // the argument block (and any step pair) has arrived
@@ -228,7 +233,7 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, int cap, float* __restr
   int qlo[NBW], qhi[NBW];
 #pragma unroll
   for (int nb = 0; nb < NBW; ++nb) {
-    const int r = rg * MFMA_ROWS + (w + 4 * nb) * 16 + col;
+    const int r = rg * MFMA_ROWS + (w + KG_WAVES * nb) * 16 + col;
     Pack8 q0, q1;
     q0.u = q1.u = make_uint4(0, 0, 0, 0);
     qlo[nb] = 0;
@@ -262,6 +267,7 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, int cap, float* __restr
   // cover 32 consecutive words of a V^T row). bf16 rows (16-bit tiles, chunk
   // pieces) are copied or byte-permuted without a float round trip.
   auto dequant = [&](const Unit& un, int st, int b) {
+    if (t >= MF_LOADERS) return;
     const bool is_v = t >= 256;
     const int kp = is_v ? (t & 31) : ((t & 255) >> 3);
     const int db = is_v ? ((t & 255) >> 5) : (t & 7);
@@ -454,6 +460,7 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, int cap, float* __restr
   if (u0 + lane < min(u1, hs.n_tiles)) win = *reinterpret_cast<const uint4*>(a.tiles + u0 + lane);
   auto unit = [&](int rel) { return unit_at(a, hs, u0 + rel, rel, h, win); };
   auto stage = [&](int st, const uint4& wk, const uint4& wv) {
+    if (t >= MF_LOADERS) return;  // a raw sub-block is at most MF_LOADERS pieces of 16 bytes
     *reinterpret_cast<uint4*>(raw_buf(st, 0) + padded(16 * t)) = wk;
     *reinterpret_cast<uint4*>(raw_buf(st, 1) + padded(16 * t)) = wv;
   };
@@ -482,7 +489,7 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, int cap, float* __restr
   // Merge the two key groups: group 1 parks (max, sum, O) in LDS (over the
   // staging buffers, once every wave is past its last unit), group 0 folds it
   // in. Lane (g, col) of block nb holds O^T rows d = 16 db + 4 g + i
-  // of local row (w + 4 nb) * 16 + col.
+  // of local row (w + KG_WAVES nb) * 16 + col.
   float lsum[NBW];
 #pragma unroll
   for (int nb = 0; nb < NBW; ++nb) {
@@ -494,7 +501,7 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, int cap, float* __restr
   if (kg == 1 && wave_on) {
 #pragma unroll
     for (int nb = 0; nb < NBW; ++nb) {
-      const int lr = (w + 4 * nb) * 16 + col;
+      const int lr = (w + KG_WAVES * nb) * 16 + col;
 #pragma unroll
       for (int db = 0; db < 4; ++db)
         *reinterpret_cast<f32x4*>(mrg_o + lr * MRG_STRIDE + 16 * db + 4 * g) = acc_o[nb][db];
@@ -506,7 +513,7 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, int cap, float* __restr
   if (kg == 0 && wave_on) {
 #pragma unroll
     for (int nb = 0; nb < NBW; ++nb) {
-      const int lr = (w + 4 * nb) * 16 + col;
+      const int lr = (w + KG_WAVES * nb) * 16 + col;
       const float2 o1 = mrg_ml[lr];
       const float mm = fmaxf(m_run[nb], o1.x);
       const float f0 = mm == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[nb] - mm);
@@ -577,12 +584,9 @@ template <int PREC>
 static void launch_prec(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml, hipStream_t s) {
   const dim3 grid(p.splits, a.heads, p.row_groups);
   const int R = (a.q_heads / a.heads) * a.nq;
-  const int rows = R < MFMA_ROWS ? R : MFMA_ROWS;  // rows of the fullest row group
-  const int nbw = ((rows + 15) / 16 + 3) / 4;       // blocks of the busiest wave
-  if (nbw >= 3)
-    hipLaunchKernelGGL((attn_mfma_kernel<PREC, 3>), grid, dim3(MF_THREADS), 0, s, a, p.units, p.splits, p.cap, part_o,
-                       part_ml);
-  else if (nbw == 2)
+  const int rows = R < MFMA_ROWS ? R : MFMA_ROWS;                 // rows of the fullest row group
+  const int nbw = ((rows + 15) / 16 + KG_WAVES - 1) / KG_WAVES;  // blocks of the busiest wave (<= 2)
+  if (nbw >= 2)
     hipLaunchKernelGGL((attn_mfma_kernel<PREC, 2>), grid, dim3(MF_THREADS), 0, s, a, p.units, p.splits, p.cap, part_o,
                        part_ml);
   else
