@@ -486,10 +486,13 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, int cap, float* __restr
   }
   DKV_TL(tl_mfma, 4);
 
-  // Merge the two key groups: group 1 parks (max, sum, O) in LDS (over the
-  // staging buffers, once every wave is past its last unit), group 0 folds it
-  // in. Lane (g, col) of block nb holds O^T rows d = 16 db + 4 g + i
+  // Merge the two key groups. Block nb of a wave is finalized by key group
+  // owner(nb) (with two blocks per wave each group finalizes one, so both
+  // groups fold and store at once); the other group parks its (max, sum, O)
+  // for that block in LDS (over the staging buffers, once every wave is past
+  // its last unit). Lane (g, col) of block nb holds O^T rows d = 16 db + 4 g + i
   // of local row (w + KG_WAVES nb) * 16 + col.
+  auto owner = [](int nb) { return NBW == 2 ? nb : 0; };
   float lsum[NBW];
 #pragma unroll
   for (int nb = 0; nb < NBW; ++nb) {
@@ -498,9 +501,10 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, int cap, float* __restr
   float* mrg_o = reinterpret_cast<float*>(smem);
   float2* mrg_ml = reinterpret_cast<float2*>(smem + MFMA_ROWS * MRG_STRIDE * 4);
   __syncthreads();
-  if (kg == 1 && wave_on) {
+  if (wave_on) {
 #pragma unroll
     for (int nb = 0; nb < NBW; ++nb) {
+      if (owner(nb) == kg) continue;  // this group finalizes the block; the other parks it
       const int lr = (w + KG_WAVES * nb) * 16 + col;
 #pragma unroll
       for (int db = 0; db < 4; ++db)
@@ -510,9 +514,10 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, int cap, float* __restr
   }
   __syncthreads();
   DKV_TL(tl_mfma, 5);
-  if (kg == 0 && wave_on) {
+  if (wave_on) {
 #pragma unroll
     for (int nb = 0; nb < NBW; ++nb) {
+      if (owner(nb) != kg) continue;
       const int lr = (w + KG_WAVES * nb) * 16 + col;
       const float2 o1 = mrg_ml[lr];
       const float mm = fmaxf(m_run[nb], o1.x);
