@@ -30,6 +30,7 @@ BITS = (4, 8, 16)
 # does (src/gpu_kernels.py:93-94,102). 'fp32': fp32-accurate (split bf16 pairs on the MFMA path).
 PRECISIONS = {'bf16': 0, 'fp32': 1}
 PATHS = {'auto': 0, 'vector': 1, 'mfma': 2, 'short': 3}
+SHORT_ROWS = 16  # query rows per KV head the short-chunk kernel takes (SHORT_ROWS of csrc/dkv_attn_common.h)
 
 
 # The kernels store bf16 or fp32 (dkv_attn_args.out_dtype, dkv_reconstruct's out_dtype); any other
@@ -105,6 +106,9 @@ class GPUCache(_CacheBase):
         self.pending_bits = 16
         self.frame_id = -1
         self.chunk_segments = None  # default `segments` of attend() (batched continuations)
+        # default `splits` of attend() for chunks of more than SHORT_ROWS query rows per KV head
+        # (0: the library's plan, the shortest latency of a launch that has the GPU to itself)
+        self.chunk_splits = 0
         self.online = plan is None
         self.plan = []  # (start, end, bits, row) per segment, as in the reference
         self.segments = []
@@ -421,6 +425,8 @@ class GPUCache(_CacheBase):
             segments = self.chunk_segments
         if segments is not None and (segments[0] != 0 or segments[-1] != n):
             raise ValueError(f'chunk segments {segments} do not cover the {n}-token chunk')
+        if splits == 0 and q.shape[1] // self.heads * n > SHORT_ROWS:
+            splits = self.chunk_splits
         out_dtype = out_dtype or q.dtype
         _check_dtype(out_dtype, 'attend output dtype')
         q, k, v = self._kv_view(q), self._kv_view(k), self._kv_view(v)
