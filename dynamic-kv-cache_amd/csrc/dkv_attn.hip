@@ -497,7 +497,7 @@ static Plan make_plan(const dkv_attn_args& a) {
       // when the kernel starts
       splits = (p.units + SHORT_UNITS - 1) / SHORT_UNITS;
     } else {
-      // MFMA: one 8-wave workgroup per CU, all resident at once (a grid one past the CU count
+      // MFMA: one 12-wave workgroup per CU, all resident at once (a grid one past the CU count
       // would take a second round for a single workgroup); balanced over the history. A launch
       // that reads its history from a device step pair (graph replays) is sized for the cap,
       // the most splits any history runs.

@@ -53,7 +53,7 @@ def bits_equal(x, y):
 
 @pytest.mark.parametrize('precision', ['bf16', 'fp32'])
 def test_noalloc_equals_attend_on_consecutive_calls(cuda, precision):
-    # a 64-token frame over 8128 tokens (51 splits per KV head), then a 5-token chunk over 1000
+    # a 64-token frame over 8128 tokens (43 splits per KV head), then a 5-token chunk over 1000
     # tokens: the second call's partials are a fraction of the first's, over the same scratch
     for past, nq, seed, out_dtype in ((8128, 64, 1, torch.float32), (1000, 5, 2, torch.bfloat16),
                                       (8128, 64, 3, torch.bfloat16)):
