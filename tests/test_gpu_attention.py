@@ -205,6 +205,38 @@ def test_split_counts_agree(cuda, splits, path):
     assert (got - oracle_out(case, dk, dv)).abs().max().item() <= 1e-3
 
 
+def test_chunk_splits_is_the_default_split_count_of_chunks(cuda):
+    """GPUCache.chunk_splits (set while pipelined frames ingest) is the split count attend() uses
+    for chunks of more than 16 query rows per KV head when the call names none: a frame chunk
+    equals the same call with splits= that count bit for bit, an explicit count still wins, and a
+    decode step (short-chunk kernel) keeps the library's plan."""
+    announce('attention chunk_splits default')
+    case = frame_chunk_case(4096, seed=21)
+    c, dk, dv = build(case, cuda)
+    q, kn, vn = (case[x][None].to(cuda) for x in ('q', 'k_new', 'v_new'))
+    c.select(16)
+    past = c.append(kn, vn, 0)
+
+    def attend(q, k, v, **kw):
+        out = c.attend(q, k, v, 0, past, out_dtype=torch.float32, precision='bf16', **kw)
+        torch.cuda.synchronize()
+        return out
+
+    plan, seven, three = attend(q, kn, vn), attend(q, kn, vn, splits=7), attend(q, kn, vn, splits=3)
+    step = attend(q[:, :, :1], kn[:, :, :1], vn[:, :, :1])
+    c.chunk_splits = 7
+    try:
+        assert torch.equal(attend(q, kn, vn), seven)
+        assert torch.equal(attend(q, kn, vn, splits=3), three)
+        assert torch.equal(attend(q[:, :, :1], kn[:, :, :1], vn[:, :, :1]), step)
+    finally:
+        c.chunk_splits = 0
+    assert not torch.equal(plan, seven)  # the counts differ in their rounding: the test can tell them apart
+    tol = max(2e-2, reference_noise(case, dk, dv))
+    err = (seven[0].cpu().double() - semantics_out(case, dk, dv, None, torch.float32)).abs().max().item()
+    assert err <= tol, (err, tol)
+
+
 @pytest.mark.parametrize('path', PATHS)
 @pytest.mark.parametrize('precision', ['fp32', 'bf16'])
 def test_more_splits_than_one_merge_pass(cuda, precision, path):
