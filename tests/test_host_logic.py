@@ -165,3 +165,22 @@ def test_chunk_segment_limit(n_segs, ok):
     else:
         with pytest.raises(ValueError, match='at most 16'):
             c.attend_args(q, kv, kv, 0, 0, out, bounds)
+
+
+def test_pipelined_frames_take_a_quarter_of_the_split_cap(monkeypatch):
+    """StreamingDecoder.group_split_count: a quarter of the library's default cap, CUs // (KV heads x
+    192-row groups), at least 1; group_splits overrides it."""
+    import types
+    from dkv.streaming import StreamingDecoder
+    monkeypatch.setattr(torch.cuda, 'get_device_properties', lambda dev: types.SimpleNamespace(multi_processor_count=256))
+
+    def count(heads, kv_heads, chunk, group_splits=None):
+        cfg = types.SimpleNamespace(num_attention_heads=heads, num_key_value_heads=kv_heads)
+        fake = types.SimpleNamespace(config=cfg, group_splits=group_splits, device='cuda:0')
+        return StreamingDecoder.group_split_count(fake, chunk)
+
+    assert count(15, 5, 64) == 12  # 256 // 5 = 51 splits, a quarter of it
+    assert count(15, 5, 16) == 12  # the 16-token prefix: still one 192-row group
+    assert count(32, 4, 64) == 5   # 8 GQA heads x 64 tokens = 512 rows, 3 row groups: 256 // 12 // 4
+    assert count(64, 64, 64) == 1  # never below one split
+    assert count(15, 5, 64, group_splits=7) == 7
