@@ -11,7 +11,9 @@ history); and the reference CPU path timed on this host (the oracle restatement)
 Every timed workload streams at least twice the 256 MB Infinity Cache (MALL) of distinct
 memory per rotation (attention: as many distinct per-layer histories as that takes; pack:
 two copies of the volume, alternated), so the bytes come from HBM. The launch floor (a graph
-of tiny dependent kernels) is reported beside the attention numbers.
+of tiny dependent kernels) is reported beside the attention numbers. The one exception is the
+reference's own attention microbenchmark (`--only ref`), replayed as the reference runs it (one
+cache-resident history, eager calls) so that its published times compare like for like.
 """
 import argparse
 import json
@@ -37,7 +39,7 @@ def parse():
     p.add_argument('--steps', type=int, default=200)
     p.add_argument('--warmup', type=int, default=20)
     p.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
-    p.add_argument('--only', choices=['pack', 'seg', 'attn', 'cand', 'e2e', 'all'], default='all')
+    p.add_argument('--only', choices=['pack', 'seg', 'attn', 'cand', 'ref', 'e2e', 'all'], default='all')
     p.add_argument('--rotate', type=int, default=48,
                    help='least number of distinct layers attention rotates over (more when the layers '
                         'hold less than 512 MB together)')
@@ -278,6 +280,57 @@ def bench_attention(past, steps, warmup, rotate, precision='bf16'):
     return dict(us_per_layer=ms * 1e3, **rot, gbs=nbytes / (ms * 1e-3) / 1e9, tflops=flops / (ms * 1e-3) / 1e12,
                 bytes=nbytes, flops=flops, mfma_frac=flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
                 hbm_frac=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, **attainable(nbytes, flops, ms))
+
+
+# The reference's published times of its own attention microbenchmark at its production tile
+# (BM 16 / BN 64), on an NVIDIA RTX 5070 Laptop GPU, ms per GPUCache.attend() call by (past, bits)
+# (results/raw/gpu_kernel_benchmark.json:36,48,156,168,276,288,396,408).
+REF_MICRO_MS = {(256, 16): 0.2581, (256, 4): 0.1737, (2048, 16): 0.1171, (2048, 4): 0.1549,
+                (4096, 16): 0.2263, (4096, 4): 0.2907, (6144, 16): 0.3320, (6144, 4): 0.4282}
+
+
+def bench_reference_micro():
+    """The reference's attention microbenchmark on this GPU (scripts/benchmark_gpu_kernels.py:8-38):
+    one layer, 3 KV / 9 Q heads, a 78-token chunk over a uniform 16-bit or 4-bit history of 256 /
+    2048 / 4096 / 6144 tokens in a planned cache [(bits, past), (16, 78)], unit-normal data. Timed
+    as the reference times it: 5 calls of warm-up, then events around 40 eager GPUCache.attend()
+    calls (host dispatch included). Also the same 40 calls replayed from one HIP graph: the GPU time
+    per call. As in the reference, every call reads the same history, which stays in the caches."""
+    import torch
+    from dkv.gpu_cache import GPUCache
+    dev = torch.device('cuda:0')
+    g = torch.Generator().manual_seed(4)
+    nq, reps, out = 78, 40, {}
+    for past in (256, 2048, 4096, 6144):
+        k, v = (torch.randn(1, 3, past, 64, generator=g).to(dev, torch.bfloat16) for _ in range(2))
+        q = torch.randn(1, 9, nq, 64, generator=g).to(dev, torch.bfloat16)
+        kn, vn = (torch.randn(1, 3, nq, 64, generator=g).to(dev, torch.bfloat16) for _ in range(2))
+        for bits in (16, 4):
+            cache = GPUCache([(bits, past), (16, nq)], layers=1, heads=3)
+            cache.select(bits)
+            cache.append(k, v, 0)
+
+            def calls(n):
+                for _ in range(n):
+                    cache.attend(q, kn, vn, 0, past)
+            calls(5)
+            torch.cuda.synchronize()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            calls(reps)
+            end.record()
+            end.synchronize()
+            eager_ms = start.elapsed_time(end) / reps
+            graph = graph_of(lambda: calls(1), reps)
+            graph_us = time_launches(graph.replay, 10, 2) / reps * 1e3
+            ref = REF_MICRO_MS[(past, bits)]
+            out[f'past_{past}_{bits}bit'] = dict(eager_ms=round(eager_ms, 4), graph_us=round(graph_us, 2),
+                                                  reference_ms=ref, eager_speedup=round(ref / eager_ms, 1))
+            print(f'# reference microbenchmark past={past} {bits}-bit: {eager_ms:.4f} ms per attend() call '
+                  f'(reference, RTX 5070 Laptop: {ref:.4f} ms), {graph_us:.2f} us per call from a graph',
+                  flush=True)
+            del graph, cache
+    return out
 
 
 def attainable(nbytes, flops, ms):
@@ -581,6 +634,8 @@ def main():
                 res['candidates'][f'{prec}_{bits}bit'] = r
                 print(f"# candidates {prec} {bits}-bit: {r['us_per_batch']:.2f} us, {r['gbs']:.0f} GB/s, "
                       f"{r['tflops']:.1f} TFLOP/s", flush=True)
+    if args.only in ('ref', 'all'):
+        res['reference_micro'] = bench_reference_micro()
     if args.only in ('e2e', 'all'):
         res['e2e'] = bench_e2e()
     cpu = None if args.no_cpu else cpu_baselines()
@@ -615,6 +670,11 @@ def main():
                               for k, r in res['candidates'].items()}
     if 'segments' in res:
         line['segments'] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in res['segments'].items()}
+    if 'reference_micro' in res:
+        line['reference_microbenchmark'] = dict(
+            workload='the reference\'s attention microbenchmark: 3 KV / 9 Q heads, 78-token chunk, uniform '
+                     '16-bit or 4-bit history, ms per attend() call over 40 eager calls; reference times from '
+                     'an RTX 5070 Laptop GPU (other hardware)', **res['reference_micro'])
     if 'e2e' in res:
         line['e2e'] = res['e2e']
     if cpu:
