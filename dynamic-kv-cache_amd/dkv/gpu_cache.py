@@ -133,6 +133,7 @@ class GPUCache(_CacheBase):
         self.tiles = torch.zeros((max(max_tiles, 1), 16), dtype=torch.uint8, device=self.device)
         self._workspace = None
         self._graph = None  # GraphSteps while launches read their step parameters from the device
+        self._fused_args, self._fused_key = None, None  # the argument block _fused_attention() reuses
         for bits, n in planned:
             if n:
                 self._open_segment(self.segments[-1].end if self.segments else 0, n, bits)
@@ -324,6 +325,51 @@ class GPUCache(_CacheBase):
         self.seen[layer] = past + n
         return q, k, v, past
 
+    def _fused_attention(self, n, q_heads, layer, qkv, qkv_stride, cos, sin, cs_stride, qkv_out, out, stream):
+        """append_projection() then attend() for the fused decoder layer's eager launches: the same
+        two launches with the same arguments (so the same bytes and outputs), without the per-call
+        checks of the general entry points, which cost more host time than the GPU spends on a
+        64-token chunk. Raw device addresses, which the caller guarantees to be what those checks
+        establish: qkv [n, (q_heads + 2 heads) * 64] and cos / sin [n, 64] bf16 rows (element
+        strides qkv_stride, cs_stride), qkv_out room for q | k | v as [heads, n, 64] blocks and out
+        for the bf16 output [1, n, q_heads, 64], all 16-byte aligned; no graph steps (eager
+        launches) and no chunk segments."""
+        H, d = self.heads, self.dim
+        past, seg, write_tiles = self._claim(layer, n)
+        kp = qkv_out + q_heads * n * d * 2
+        vp = kp + H * n * d * 2
+        head = n * d  # element stride of the heads of q, k and v
+        job = _lib.PackJob(kp, vp, head, d, head, d, seg.offset, seg.rows, seg.start, past - seg.start,
+                           n, layer, seg.bits, seg.tile0, write_tiles)
+        lib = _lib.load()
+        _lib.check(lib.dkv_rope_pack(qkv, qkv_stride, cos, sin, cs_stride, n, q_heads, qkv_out, kp, vp,
+                                     ctypes.byref(job), 0, self.arena.data_ptr(), self.arena_bytes,
+                                     self.tiles.data_ptr(), self.layers, H, stream), 'dkv_rope_pack')
+        self.seen[layer] = past + n
+        a = self._fused_args
+        if a is None or self._fused_key != (n, q_heads):
+            # the fields that stay the same while the chunk shape does (attend_args() sets them alike)
+            a = self._fused_args = _lib.AttnArgs()
+            self._fused_key = (n, q_heads)
+            a.q_head_stride = a.kn_head_stride = a.vn_head_stride = head
+            a.q_tok_stride = a.kn_tok_stride = a.vn_tok_stride = d
+            a.layers, a.heads, a.q_heads, a.nq = self.layers, H, q_heads, n
+            a.scale = d ** -0.5
+            a.out_tok_stride, a.out_head_stride = q_heads * d, d
+        a.q, a.k_new, a.v_new, a.out = qkv_out, kp, vp, out
+        a.arena, a.tiles = self.arena.data_ptr(), self.tiles.data_ptr()
+        a.n_tiles, a.past, a.layer = self._tiles_before(past), past, layer
+        a.precision = PRECISIONS[self.precision]
+        if q_heads // H * n > SHORT_ROWS:
+            a.splits = self.chunk_splits
+        need = lib.dkv_attend_workspace_bytes(ctypes.byref(a))
+        if need:
+            ws = self._workspace_for(need)
+            a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+        else:
+            a.workspace, a.workspace_bytes = None, 0
+        _lib.check(lib.dkv_attend(ctypes.byref(a), stream), 'dkv_attend')
+
     def append_batch(self, k, v, bits, lengths):
         """Appends several segments for every layer in one pack launch.
 
@@ -484,6 +530,7 @@ class GPUCache(_CacheBase):
         other.host_counts = self.host_counts.copy()
         other._workspace = None
         other._graph = None
+        other._fused_args, other._fused_key = None, None
         other.pending_bits = 16
         return other
 

@@ -140,25 +140,124 @@ def linear(x, weight, norm=None, eps=1e-6, residual=None, silu_mul=False):
     return out.view(*x.shape[:-1], n_out)
 
 
+class _LayerPlan:
+    """What fused_decoder_layer checked once for one decoder layer and chunk length, and the
+    constant arguments of its launches: the weight and norm tensors it checked (a layer that holds
+    other objects gets a new plan; their data pointers are read at every launch, since moving a
+    module swaps a parameter's storage in place), their row strides and row counts, the norm
+    epsilons and the head counts."""
+    __slots__ = ('qkv_w', 'o_w', 'gu_w', 'd_w', 'ln1_w', 'ln2_w', 'qkv_args', 'o_args', 'gu_args', 'd_args',
+                 'eps1', 'eps2', 'q_heads', 'kv_heads', 'eager_ok', 'layer_idx', 'width', 'inter')
+
+    def holds(self, layer):
+        # the modules' own dicts: nn.Module attribute lookups cost more than the rest of this check
+        m = layer._modules
+        attn, mlp = m['self_attn'], m['mlp']
+        return (self.qkv_w is attn._qkv_weight and self.gu_w is mlp._gate_up_weight
+                and self.o_w is attn._modules['o_proj']._parameters['weight']
+                and self.d_w is mlp._modules['down_proj']._parameters['weight']
+                and self.ln1_w is m['input_layernorm']._parameters['weight']
+                and self.ln2_w is m['post_attention_layernorm']._parameters['weight'])
+
+
+def _layer_plan(layer, n, width):
+    """The _LayerPlan of (layer, n) (built on first use), or None when dkv_linear does not cover the
+    layer's projections at n rows."""
+    plans = layer.__dict__.setdefault('_dkv_plans', {})
+    attn, mlp = layer.self_attn, layer.mlp
+    p = plans.get((n, width))
+    if p is not None and p.holds(layer):
+        return p
+    ln1, ln2 = layer.input_layernorm, layer.post_attention_layernorm
+    o_w, d_w = attn.o_proj.weight, mlp.down_proj.weight
+    if not (attn.o_proj.bias is None and mlp.down_proj.bias is None
+            and getattr(ln1, 'weight', None) is not None and getattr(ln2, 'weight', None) is not None
+            and linear_covered(n, attn._qkv_weight, True, LINEAR_PLAIN)
+            and linear_covered(n, o_w, False, LINEAR_RESIDUAL) and o_w.shape[0] == width
+            and linear_covered(n, mlp._gate_up_weight, True, LINEAR_SILU_MUL)
+            and linear_covered(n, d_w, False, LINEAR_RESIDUAL) and d_w.shape[0] == width
+            and all(_fused(w) and w.dim() == 1 and w.stride(0) == 1 and w.data_ptr() % 16 == 0
+                    for w in (ln1.weight, ln2.weight))):
+        plans[(n, width)] = None
+        return None
+    p = _LayerPlan()
+    p.qkv_w, p.o_w, p.gu_w, p.d_w = attn._qkv_weight, o_w, mlp._gate_up_weight, d_w
+    p.ln1_w, p.ln2_w = ln1.weight, ln2.weight
+    p.eps1, p.eps2 = float(ln1.variance_epsilon), float(ln2.variance_epsilon)
+    # (weight, row stride, weight rows, k) of each dkv_linear launch
+    p.qkv_args = (p.qkv_w, p.qkv_w.stride(0), p.qkv_w.shape[0], p.qkv_w.shape[1])
+    p.o_args = (o_w, o_w.stride(0), o_w.shape[0], o_w.shape[1])
+    p.gu_args = (p.gu_w, p.gu_w.stride(0), p.gu_w.shape[0], p.gu_w.shape[1])
+    p.d_args = (d_w, d_w.stride(0), d_w.shape[0], d_w.shape[1])
+    sizes, hd = attn._qkv_sizes, attn.head_dim
+    p.q_heads, p.kv_heads = sizes[0] // hd, sizes[1] // hd
+    # the eager launches split q | k | v as dkv_rope_pack does: 64-wide heads, K and V alike
+    p.eager_ok = hd == 64 and sizes[1] == sizes[2] and p.qkv_w.shape[0] == sum(sizes) and sizes[0] % hd == 0
+    p.layer_idx, p.width, p.inter = attn.layer_idx, width, p.gu_w.shape[0] // 2
+    plans[(n, width)] = p
+    return p
+
+
+def _fused_layer_eager(p, h, n, cache, cos, sin):
+    """The fused layer's eager launches for a checked plan: the launches and arguments linear() and
+    attend_projection() would make, without their per-call checks (which cost more host time than
+    the GPU spends on a 64-token chunk). The intermediates (the joined projection, q | k | v, the
+    attention output, the post-attention residual, SiLU*up) share one allocation; the kernels read
+    and write it in stream order, and the allocator hands it out again only to later work on the
+    same stream."""
+    lib = _lib.load()
+    stream = _lib.stream_handle(h.device)
+    width, inter = p.width, p.inter
+    qw, qld, qrows, qk = p.qkv_args
+    ow, old, orows, ok = p.o_args
+    gw, gld, grows, gk = p.gu_args
+    dw, dld, drows, dk = p.d_args
+    # element offsets of [qkv | q,k,v | attention out | h2 | act], each n rows (multiples of 64 columns)
+    o_qkvo = n * qrows
+    o_att = o_qkvo + n * qrows
+    o_h2 = o_att + n * ok
+    o_act = o_h2 + n * orows
+    scratch = torch.empty(o_act + n * inter, dtype=torch.bfloat16, device=h.device)
+    out = torch.empty((1, n, drows), dtype=torch.bfloat16, device=h.device)
+    base = scratch.data_ptr()
+    xp, qkv, att, h2, act = h.data_ptr(), base, base + 2 * o_att, base + 2 * o_h2, base + 2 * o_act
+    _lib.check(lib.dkv_linear(xp, width, qw.data_ptr(), qld, n, qrows, qk, p.ln1_w.data_ptr(), p.eps1, LINEAR_PLAIN,
+                              None, 0, qkv, qrows, stream), 'dkv_linear')
+    cache._fused_attention(n, p.q_heads, p.layer_idx, qkv, qrows, cos.data_ptr(), sin.data_ptr(), cos.stride(0),
+                           base + 2 * o_qkvo, att, stream)
+    _lib.check(lib.dkv_linear(att, ok, ow.data_ptr(), old, n, orows, ok, None, 1e-6, LINEAR_RESIDUAL, xp, width,
+                              h2, orows, stream), 'dkv_linear')
+    _lib.check(lib.dkv_linear(h2, width, gw.data_ptr(), gld, n, grows, gk, p.ln2_w.data_ptr(), p.eps2,
+                              LINEAR_SILU_MUL, None, 0, act, inter, stream), 'dkv_linear')
+    _lib.check(lib.dkv_linear(act, inter, dw.data_ptr(), dld, n, drows, dk, None, 1e-6, LINEAR_RESIDUAL, h2, width,
+                              out.data_ptr(), drows, stream), 'dkv_linear')
+    return out
+
+
 def fused_decoder_layer(layer, hidden_states, cache, position_embeddings):
     """One LlamaDecoderLayer forward on a packed GPUCache as six launches plus the attention's
-    two; None when the layer, the inputs or the cache are outside what they cover."""
+    two; None when the layer, the inputs or the cache are outside what they cover. What depends
+    only on the layer and the chunk length is checked once (_layer_plan); eager launches on
+    contiguous inputs then take _fused_layer_eager, and graph captures the general path below."""
     from .gpu_cache import GPUCache, attend_projection
-    attn, mlp = layer.self_attn, layer.mlp
-    ln1, ln2 = layer.input_layernorm, layer.post_attention_layernorm
+    attn, mlp = layer._modules['self_attn'], layer._modules['mlp']
     h = hidden_states
     if not (isinstance(cache, GPUCache) and cache.backend == 'fused' and position_embeddings is not None
             and hasattr(attn, '_qkv_weight') and hasattr(mlp, '_gate_up_weight') and h.dim() == 3
-            and h.shape[0] == 1 and _fused(h) and attn.o_proj.bias is None and mlp.down_proj.bias is None
-            and getattr(ln1, 'weight', None) is not None and getattr(ln2, 'weight', None) is not None):
+            and h.shape[0] == 1 and _fused(h)):
         return None
     n, width = h.shape[1], h.shape[2]
-    o_w, d_w = attn.o_proj.weight, mlp.down_proj.weight
-    if not (linear_covered(n, attn._qkv_weight, True, LINEAR_PLAIN)
-            and linear_covered(n, o_w, False, LINEAR_RESIDUAL) and o_w.shape[0] == width
-            and linear_covered(n, mlp._gate_up_weight, True, LINEAR_SILU_MUL)
-            and linear_covered(n, d_w, False, LINEAR_RESIDUAL) and d_w.shape[0] == width):
+    p = _layer_plan(layer, n, width)
+    if p is None:
         return None
+    if p.eager_ok and p.kv_heads == cache.heads and cache._graph is None and cache.chunk_segments is None:
+        cos, sin = position_embeddings
+        if (h.is_contiguous() and h.data_ptr() % 16 == 0 and cos.shape == (1, n, 64) and sin.shape == cos.shape
+                and cos.dtype == torch.bfloat16 and sin.dtype == torch.bfloat16 and cos.is_contiguous()
+                and sin.is_contiguous() and cos.data_ptr() % 16 == 0 and sin.data_ptr() % 16 == 0):
+            return _fused_layer_eager(p, h, n, cache, cos.view(n, 64), sin.view(n, 64))
+    ln1, ln2 = layer.input_layernorm, layer.post_attention_layernorm
+    o_w, d_w = attn.o_proj.weight, mlp.down_proj.weight
     x = h.reshape(n, width)
     qkv = linear(x, attn._qkv_weight, norm=ln1.weight, eps=ln1.variance_epsilon)
     o = attend_projection(attn, cache, qkv.view(1, n, -1), position_embeddings)
