@@ -138,3 +138,43 @@ def test_fused_layers_match_upstream_layers(cuda):
     torch.cuda.synchronize()
     diff = (out[True] - out[False]).abs().max().item()
     assert diff <= 0.05, diff
+
+
+def test_eager_fused_layers_follow_weight_changes(cuda):
+    """The eager fused layers check a layer once per chunk length and keep its weight objects, reading
+    their data pointers at every call: a weight whose storage moves (param.data replaced, as
+    Module.to() does) and a weight replaced by a new Parameter are both used by the next forward.
+    Logits change and stay within 0.05 of the upstream layers with the new weights."""
+    announce('linear: eager fused layers follow weight changes')
+    from dkv.streaming import StreamingDecoder, build_decoder
+    model = build_decoder(layers=2, hidden=384, heads=6, kv_heads=2, intermediate=768, vocab=512, seed=23)
+    dec = StreamingDecoder(model, precision='fp32')
+    g = torch.Generator().manual_seed(24)
+    prefix = torch.randint(0, 512, (1, 16), generator=g)
+    question = torch.randint(0, 512, (1, 24), generator=g)
+    ids = torch.randint(0, 512, (1, 64), generator=g).to(cuda)
+    with torch.inference_mode():
+        emb = model.model.get_input_embeddings()(ids)
+    cache = dec.ingest(prefix, [emb], [8])
+
+    def logits(layers):
+        dec.ops_state['layers'] = layers
+        try:
+            out = dec.forward(cache.fork(), ids=question, logits=question.shape[1])
+        finally:
+            dec.ops_state['layers'] = True
+        torch.cuda.synchronize()
+        return out
+
+    before = logits(True)
+    layer = model.model.layers[1]
+    with torch.no_grad():
+        layer.mlp.down_proj.weight.data = layer.mlp.down_proj.weight.data * 2  # same Parameter, new storage
+        layer.self_attn.o_proj.weight = torch.nn.Parameter(layer.self_attn.o_proj.weight.detach() * 0.5,
+                                                           requires_grad=False)
+    fused, upstream = logits(True), logits(False)
+    changed = (fused - before).abs().max().item()
+    diff = (fused - upstream).abs().max().item()
+    print(f'[fused-weights] change {changed:.3e}, fused vs upstream {diff:.3e}', flush=True)
+    assert changed > 1e-2, changed
+    assert diff <= 0.05, diff
