@@ -487,6 +487,12 @@ static Plan make_plan(const dkv_attn_args& a) {
   p.precision = a.precision;
   p.rows_per_group = p.path == 3 ? SHORT_ROWS : (p.path == 2 ? MFMA_ROWS : VEC_ROWS);
   p.row_groups = (R + p.rows_per_group - 1) / p.rows_per_group;
+  if (p.path == 2) {
+    // The same number of groups, balanced: 16-row blocks spread evenly, so that no group (the
+    // critical path of every unit) carries more blocks than it must. At most MFMA_ROWS rows.
+    const int blocks = (R + 15) / 16;
+    p.rows_per_group = 16 * ((blocks + p.row_groups - 1) / p.row_groups);
+  }
   p.units = a.n_tiles + (a.nq + TILE - 1) / TILE;
   int splits = a.splits;
   p.cap = 0;

@@ -197,7 +197,7 @@ static __device__ uint64_t tl_mfma[TL_SLOTS * TL_EVENTS];
 
 template <int PREC, int NBW>
 __global__ void __launch_bounds__(MF_THREADS)
-attn_mfma_kernel(dkv_attn_args a, int units, int splits, int cap, float* __restrict__ part_o,
+attn_mfma_kernel(dkv_attn_args a, int units, int splits, int cap, int rpg, float* __restrict__ part_o,
                  float2* __restrict__ part_ml) {
   // LDS: two raw stages of (K, V) sub-blocks and two sets of bf16 tiles
   // (K, V^T, and for PREC 1 their lo parts). After the last unit the same
@@ -226,19 +226,22 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, int cap, float* __restr
   const int u0 = (int)((int64_t)units * split / active);
   const int u1 = (int)((int64_t)units * (split + 1) / active);
   const float xs = a.scale * LOG2E;
-  const bool wave_on = rg * MFMA_ROWS + w * 16 < R;  // wave-uniform
+  // Row group rg holds rows [r0, r_end): rpg rows (a multiple of 16, at most MFMA_ROWS), the
+  // last group fewer.
+  const int r0 = rg * rpg, r_end = min(R, r0 + rpg);
+  const bool wave_on = r0 + w * 16 < r_end;  // wave-uniform
 
   // Query operands and masking bounds of this lane's query column in each block.
   bf16x8 qop[NBW][2];
   int qlo[NBW], qhi[NBW];
 #pragma unroll
   for (int nb = 0; nb < NBW; ++nb) {
-    const int r = rg * MFMA_ROWS + (w + KG_WAVES * nb) * 16 + col;
+    const int r = r0 + (w + KG_WAVES * nb) * 16 + col;
     Pack8 q0, q1;
     q0.u = q1.u = make_uint4(0, 0, 0, 0);
     qlo[nb] = 0;
     qhi[nb] = -1;
-    if (r < R) {
+    if (r < r_end) {
       const int gq = r / a.nq, m = r - gq * a.nq;
       const uint16_t* src = static_cast<const uint16_t*>(a.q) + (int64_t)(h * G + gq) * a.q_head_stride +
                             (int64_t)m * a.q_tok_stride + 8 * g;
@@ -524,12 +527,12 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, int cap, float* __restr
       const float f0 = mm == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[nb] - mm);
       const float f1 = mm == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(o1.x - mm);
       float l = lsum[nb] * f0 + o1.y * f1;
-      const int r = rg * MFMA_ROWS + lr;
+      const int r = r0 + lr;
       f32x4 o[4];
 #pragma unroll
       for (int db = 0; db < 4; ++db)
         o[db] = acc_o[nb][db] * f0 + *reinterpret_cast<const f32x4*>(mrg_o + lr * MRG_STRIDE + 16 * db + 4 * g) * f1;
-      if (r >= R) continue;
+      if (r >= r_end) continue;
       if (active == 1) {  // the splits that run (see attn_vec_kernel's epilogue)
         const int gq = r / a.nq, m = r - gq * a.nq;
         const float inv = 1.f / l;
@@ -588,15 +591,13 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, int cap, float* __restr
 template <int PREC>
 static void launch_prec(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml, hipStream_t s) {
   const dim3 grid(p.splits, a.heads, p.row_groups);
-  const int R = (a.q_heads / a.heads) * a.nq;
-  const int rows = R < MFMA_ROWS ? R : MFMA_ROWS;                 // rows of the fullest row group
-  const int nbw = ((rows + 15) / 16 + KG_WAVES - 1) / KG_WAVES;  // blocks of the busiest wave (<= 2)
+  const int nbw = (p.rows_per_group / 16 + KG_WAVES - 1) / KG_WAVES;  // blocks of the busiest wave (<= 2)
   if (nbw >= 2)
-    hipLaunchKernelGGL((attn_mfma_kernel<PREC, 2>), grid, dim3(MF_THREADS), 0, s, a, p.units, p.splits, p.cap, part_o,
-                       part_ml);
+    hipLaunchKernelGGL((attn_mfma_kernel<PREC, 2>), grid, dim3(MF_THREADS), 0, s, a, p.units, p.splits, p.cap,
+                       p.rows_per_group, part_o, part_ml);
   else
-    hipLaunchKernelGGL((attn_mfma_kernel<PREC, 1>), grid, dim3(MF_THREADS), 0, s, a, p.units, p.splits, p.cap, part_o,
-                       part_ml);
+    hipLaunchKernelGGL((attn_mfma_kernel<PREC, 1>), grid, dim3(MF_THREADS), 0, s, a, p.units, p.splits, p.cap,
+                       p.rows_per_group, part_o, part_ml);
 }
 
 int launch_attn_mfma(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml, hipStream_t s) {

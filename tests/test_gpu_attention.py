@@ -195,6 +195,32 @@ def test_chunk_lengths(cuda, nq, path):
     assert (got - oracle_out(case, dk, dv)).abs().max().item() <= 1e-3
 
 
+@pytest.mark.parametrize('heads,group,nq', [(3, 3, 78), (2, 4, 64), (2, 3, 65), (1, 4, 97)])
+def test_balanced_row_groups(cuda, heads, group, nq):
+    """More than 192 query rows per KV head are split over equal groups of whole 16-row blocks
+    (234 rows: 128 + 106; 256: 128 + 128; 195: 112 + 83; 388: 144 + 144 + 100), each group's
+    waves past its last row idle: fp32 precision within 1e-3 of the oracle at one split and at the
+    default count, bf16 precision at one split within the reference's p-rounding noise."""
+    announce(f'attention balanced row groups heads={heads} group={group} nq={nq}')
+    case = frame_chunk_case(900, seed=40 + nq, heads=heads, q_heads=heads * group, nq=nq)
+    c, dk, dv = build(case, cuda)
+    ref = oracle_out(case, dk, dv)
+    q, kn, vn = (case[x][None].to(cuda) for x in ('q', 'k_new', 'v_new'))
+    c.select(16)
+    p0 = c.append(kn, vn, 0)
+    for splits in (1, 0):
+        got = c.attend(q, kn, vn, 0, p0, out_dtype=torch.float32, path='mfma', splits=splits, precision='fp32')
+        err = (got[0].cpu().double() - ref).abs().max().item()
+        assert err <= 1e-3, (splits, err)
+    got = c.attend(q, kn, vn, 0, p0, out_dtype=torch.float32, path='mfma', splits=1,
+                   precision='bf16')[0].cpu().double()
+    err = (got - semantics_out(case, dk, dv, None, torch.float32)).abs().max().item()
+    noise = reference_noise(case, dk, dv, None)
+    print(f'[bf16-vs-reference] balanced row groups {heads}x{group}x{nq}: max-abs {err:.4e}, '
+          f'noise {noise:.4e}', flush=True)
+    assert err <= max(2e-2, noise), (err, noise)
+
+
 @pytest.mark.parametrize('path', PATHS)
 @pytest.mark.parametrize('splits', [1, 3, 1000])
 def test_split_counts_agree(cuda, splits, path):
