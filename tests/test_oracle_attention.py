@@ -146,6 +146,37 @@ def test_reference_semantics_blocks_without_rescaling():
     assert torch.allclose(got, expect, rtol=1e-6, atol=1e-6)
 
 
+def test_reference_semantics_rounds_p_against_the_running_max():
+    """The reference rounds p to bf16 against the maximum known when a block is processed and
+    rescales the accumulated P.V by alpha in fp32 afterwards (src/gpu_kernels.py:97-102). A case
+    whose every score is exact: block 0 holds 32 keys of score 1 (V = 1) and 32 of score 0 (V = 2),
+    block 1 raises the maximum to 3 (64 keys, V = -1), the chunk's own key scores 3 (V = -1).
+    Block 0's p are 1 and bf16(e^-1), scaled by e^-2 when block 1 arrives, so the output is
+    ((32 + 64 bf16(e^-1)) e^-2 - 65) / ((32 + 32 e^-1) e^-2 + 65). Rounding p against the final
+    maximum instead, or not rounding it, gives values 2.8e-4 and 8.5e-5 away."""
+    past = 128
+    q = torch.zeros(1, 1, 64)
+    q[0, 0, 0] = 8.0  # score = 8 * k[0] * 0.125 = k[0]
+    k = torch.zeros(1, past + 1, 64)
+    v = torch.zeros(1, past + 1, 64)
+    k[0, 0:64:2, 0], v[0, 0:64:2] = 1.0, 1.0
+    k[0, 1:64:2, 0], v[0, 1:64:2] = 0.0, 2.0
+    k[0, 64:, 0], v[0, 64:] = 3.0, -1.0
+    got = reference_semantics(q.bfloat16(), k, v, past, out_dtype=torch.float32)[0, 0].double()
+
+    def bf16(x):
+        return float(torch.tensor(x).bfloat16())
+
+    e1, e2 = math.exp(-1), math.exp(-2)
+    den = (32 + 32 * e1) * e2 + 65
+    expect = ((32 + 64 * bf16(e1)) * e2 - 65) / den
+    late = (32 * bf16(e2) + 64 * bf16(math.exp(-3)) - 65) / den
+    unrounded = ((32 + 64 * e1) * e2 - 65) / den
+    assert torch.allclose(got, torch.full((64,), expect, dtype=torch.float64), rtol=1e-6, atol=0)
+    for wrong in (late, unrounded):
+        assert (got - wrong).abs().min().item() > 5e-5
+
+
 def test_reference_semantics_segments_equal_separate_calls():
     g = torch.Generator().manual_seed(32)
     past, bounds = 70, [0, 4, 9]
