@@ -111,6 +111,17 @@ __device__ __forceinline__ int runtime_plan(const dkv_attn_args& a, Hist& hs, in
 // kernel's partials applies the same rule.
 __device__ __forceinline__ int short_runtime_plan(const dkv_attn_args& a, Hist& hs, int& units, int nwg);
 
+// max(a, b) of values that are never NaN (scores, running maxima, -inf masks) in one
+// instruction, v_med3_f32(a, b, +inf). fmaxf has to quiet signalling NaN operands first, an extra
+// v_max_f32 x, x, x per operand the compiler cannot prove canonical (MFMA results, lane swaps);
+// so would med3 with a literal +inf, which the optimizer folds back into fmaxf. The empty asm
+// makes +inf an SGPR value it cannot see through (it emits no instruction).
+__device__ __forceinline__ float max_nn(float a, float b) {
+  float inf;
+  asm("" : "=s"(inf) : "0"(INFINITY));
+  return __builtin_amdgcn_fmed3f(a, b, inf);
+}
+
 // First chunk row of the segment holding chunk row j (0 when n_segs <= 1).
 __device__ __forceinline__ int chunk_seg_start(const dkv_attn_args& a, int j) {
   int start = 0;

@@ -85,9 +85,9 @@ __device__ __forceinline__ float bf16_hi_f(uint32_t w) { return __uint_as_float(
 // x[l mod 32 + 32]), after permlane16_swap (x[row 2k], x[row 2k + 1]).
 __device__ __forceinline__ float group_max(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  x = max_nn(__uint_as_float(r[0]), __uint_as_float(r[1]));
   auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+  return max_nn(__uint_as_float(q[0]), __uint_as_float(q[1]));
 }
 __device__ __forceinline__ float group_sum(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -115,7 +115,10 @@ __device__ __forceinline__ void dequant8(const uint8_t* raw, int bits, int rows,
   float q[8];
   if (bits == 4) {
     const uint32_t w = *reinterpret_cast<const uint32_t*>(raw + padded(r * 32 + db * 4));
-    const uint32_t ev = w & 0x0f0f0f0fu, od = (w >> 4) & 0x0f0f0f0fu;  // even / odd elements
+    uint32_t ev = w & 0x0f0f0f0fu, od = (w >> 4) & 0x0f0f0f0fu;  // even / odd elements
+    // Opaque to the optimizer (no instruction), which would otherwise fold each byte back into a
+    // nibble extract of w (v_bfe, then a convert) instead of one v_cvt_f32_ubyteN per element.
+    asm("" : "+v"(ev), "+v"(od));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       q[2 * i] = (float)((ev >> (8 * i)) & 255u);
@@ -166,12 +169,25 @@ __device__ __forceinline__ void raw_load(const dkv_attn_args& a, const Unit& un,
 // scalar load; later tiles fall back to reading the table.
 __device__ __forceinline__ Unit unit_at(const dkv_attn_args& a, const Hist& hs, int u, int rel, int h,
                                         const uint4& win) {
-  if (u >= hs.n_tiles || rel >= 64) return get_unit(a, hs, u, h);
+  if (u >= hs.n_tiles) return get_unit(a, hs, u, h);
   Unit un;
-  const int64_t off = (int64_t)((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)win.y, rel) << 32 |
-                                (uint32_t)__builtin_amdgcn_readlane((int)win.x, rel));
-  const int tok = __builtin_amdgcn_readlane((int)win.z, rel);
-  const uint32_t w3 = (uint32_t)__builtin_amdgcn_readlane((int)win.w, rel);
+  uint32_t w0, w1, w2, w3;
+  if (rel < 64) {
+    w0 = (uint32_t)__builtin_amdgcn_readlane((int)win.x, rel);
+    w1 = (uint32_t)__builtin_amdgcn_readlane((int)win.y, rel);
+    w2 = (uint32_t)__builtin_amdgcn_readlane((int)win.z, rel);
+    w3 = (uint32_t)__builtin_amdgcn_readlane((int)win.w, rel);
+  } else {
+    // past the window: the whole descriptor in one 16-byte load (not four narrow ones, whose
+    // destination registers would make every iteration wait on the loads in flight)
+    const uint4 d = *reinterpret_cast<const uint4*>(a.tiles + u);
+    w0 = __builtin_amdgcn_readfirstlane(d.x);
+    w1 = __builtin_amdgcn_readfirstlane(d.y);
+    w2 = __builtin_amdgcn_readfirstlane(d.z);
+    w3 = __builtin_amdgcn_readfirstlane(d.w);
+  }
+  const int64_t off = (int64_t)((uint64_t)w1 << 32 | w0);
+  const int tok = (int)w2;
   const int rows = (int)(w3 & 0xffffu), bits = (int)((w3 >> 16) & 0xffu);
   un.chunk = false;
   un.first = tok;
@@ -297,14 +313,21 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, int cap, int rpg, float
       return;
     }
     float x0[8], x1[8];
-    if (ok0) dequant8(raw, un.bits, un.rows, r0, db, x0);
-    else
+    if (un.valid == TILE) {  // wave-uniform: every row of a full tile is valid
+      dequant8(raw, un.bits, un.rows, r0, db, x0);
+      dequant8(raw, un.bits, un.rows, r1, db, x1);
+    } else {
+      // rows past `valid` hold stale staging bytes; they become zeros (P is 0 there, and a
+      // stale NaN would still poison P.V)
+      if (ok0) dequant8(raw, un.bits, un.rows, r0, db, x0);
+      else
 #pragma unroll
-      for (int i = 0; i < 8; ++i) x0[i] = 0.f;
-    if (ok1) dequant8(raw, un.bits, un.rows, r1, db, x1);
-    else
+        for (int i = 0; i < 8; ++i) x0[i] = 0.f;
+      if (ok1) dequant8(raw, un.bits, un.rows, r1, db, x1);
+      else
 #pragma unroll
-      for (int i = 0; i < 8; ++i) x1[i] = 0.f;
+        for (int i = 0; i < 8; ++i) x1[i] = 0.f;
+    }
     if (!is_v) {
       uint16_t* k_hi = tile(b, 0);
       uint16_t* k_lo = tile(b, PREC ? 2 : 0);
@@ -398,13 +421,13 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, int cap, int rpg, float
 #pragma unroll
         for (int e = 0; e < 8; ++e) s[e] = (e >= lo && e < hi) ? s[e] : -INFINITY;
       }
-      float mt = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+      float mt = max_nn(max_nn(max_nn(s[0], s[1]), max_nn(s[2], s[3])), max_nn(max_nn(s[4], s[5]), max_nn(s[6], s[7])));
       const float mcand = group_max(mt) * xs;
       // Lazy rescaling: a wave moves its running maxima (and rescales its
       // accumulators) only when some column's max grew by more than
       // rescale_log2; otherwise p = 2^(x - m_run) <= 2^rescale_log2.
       if (__builtin_amdgcn_ballot_w64(mcand > m_run[nb] + rescale_log2<PREC>())) {
-        const float mnew = fmaxf(m_run[nb], mcand);
+        const float mnew = max_nn(m_run[nb], mcand);
         const float alpha = mnew == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run[nb] - mnew);
         m_run[nb] = mnew;
         l_part[nb] *= alpha;

@@ -62,9 +62,9 @@ __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 
 // Max / sum over the four lanes col, col + 16, col + 32, col + 48 (one query column).
 __device__ __forceinline__ float col_max(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  x = max_nn(__uint_as_float(r[0]), __uint_as_float(r[1]));
   auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+  return max_nn(__uint_as_float(q[0]), __uint_as_float(q[1]));
 }
 __device__ __forceinline__ float col_sum(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -296,10 +296,10 @@ attn_short_kernel(dkv_attn_args a, int units, int nwg, float* __restrict__ part_
       }
     float mt = s[0];
 #pragma unroll
-    for (int e = 1; e < 8; ++e) mt = fmaxf(mt, s[e]);
+    for (int e = 1; e < 8; ++e) mt = max_nn(mt, s[e]);
     const float mcand = col_max(mt) * xs;
     if (__builtin_amdgcn_ballot_w64(mcand > m_run + (PREC ? 8.f : 0.f))) {
-      const float mnew = fmaxf(m_run, mcand);
+      const float mnew = max_nn(m_run, mcand);
       const float alpha = mnew == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - mnew);
       m_run = mnew;
       l_part *= alpha;
