@@ -484,6 +484,9 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, int cap, int rpg, float
   const int n = u1 - u0;
   uint4 win = make_uint4(0, 0, 0, 0);
   if (u0 + lane < min(u1, hs.n_tiles)) win = *reinterpret_cast<const uint4*>(a.tiles + u0 + lane);
+  // Wait for the window here, on every path (unit 0 reads it next anyway): a wait the compiler
+  // cannot place before the loop lands inside it, where it also waits for the prefetches in flight.
+  asm volatile("" ::"v"(win.x), "v"(win.y), "v"(win.z), "v"(win.w));
   auto unit = [&](int rel) { return unit_at(a, hs, u0 + rel, rel, h, win); };
   auto stage = [&](int st, const uint4& wk, const uint4& wv) {
     if (t >= MF_LOADERS) return;  // a raw sub-block is at most MF_LOADERS pieces of 16 bytes
@@ -494,6 +497,10 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, int cap, int rpg, float
   if (n > 0) raw_load(a, unit(0), h, wk0, wv0);
   if (n > 1) raw_load(a, unit(1), h, wk, wv);  // in flight while unit 0 is staged
   if (n > 0) stage(0, wk0, wv0);
+  // unit 0's load registers are settled on every path before the loop (the compiler does not
+  // tie the two n > 0 tests together and would otherwise wait on them inside the loop, where a
+  // wait also drains the prefetches in flight)
+  asm volatile("" ::"v"(wk0.x), "v"(wk0.y), "v"(wk0.z), "v"(wk0.w), "v"(wv0.x), "v"(wv0.y), "v"(wv0.z), "v"(wv0.w));
   DKV_TL(tl_mfma, 1);
   __syncthreads();
   if (n > 0) dequant(unit(0), 0, 0);
