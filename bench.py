@@ -6,7 +6,9 @@ seeded 4/8/16-bit widths), in algorithmic GB/s = (bytes read + bytes written) / 
 Also reported on the same line: frame-chunk attention (15 Q / 5 KV heads, 64-token
 causal chunk over 1024/4096/8128-token mixed histories) in us/layer, GB/s and TFLOP/s;
 candidate scoring (4 continuations of 8-24 tokens over a 6144-token 4-bit / 8-bit
-history); and the reference CPU path timed on this host (the oracle restatement).
+history); the same attention workloads as independent launches in flight together over 8
+streams (`--only tput`: what the kernels sustain once launch latency overlaps); and the
+reference CPU path timed on this host (the oracle restatement).
 
 Every timed workload streams at least twice the 256 MB Infinity Cache (MALL) of distinct
 memory per rotation (attention: as many distinct per-layer histories as that takes; pack:
@@ -39,7 +41,7 @@ def parse():
     p.add_argument('--steps', type=int, default=200)
     p.add_argument('--warmup', type=int, default=20)
     p.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
-    p.add_argument('--only', choices=['pack', 'seg', 'attn', 'cand', 'ref', 'e2e', 'all'], default='all')
+    p.add_argument('--only', choices=['pack', 'seg', 'attn', 'cand', 'ref', 'tput', 'e2e', 'all'], default='all')
     p.add_argument('--rotate', type=int, default=48,
                    help='least number of distinct layers attention rotates over (more when the layers '
                         'hold less than 512 MB together)')
@@ -207,10 +209,13 @@ def rotation_layers(bits, lengths, least):
     return max(least, -(-ROTATION_BYTES // per))
 
 
-def attention_setup(past, rotate, bits, nq=64, segments=None, seed=0, precision='bf16', path='auto', splits=0):
+def attention_setup(past, rotate, bits, nq=64, segments=None, seed=0, precision='bf16', path='auto', splits=0,
+                    streams=1):
     """`rotate` layers, each with its own copy of one seeded history, and one graph that runs
-    the attention of every layer once (distinct histories, so the reads come from HBM). Returns
-    (replay, bytes per layer, kept objects); keep['rotate'] is the layer count."""
+    the attention of every layer once (distinct histories, so the reads come from HBM). With
+    streams > 1 the layers are dealt round-robin to that many streams forked inside the graph,
+    each with its own workspace, so independent launches overlap (as requests or pipelined frames
+    would). Returns (replay, bytes per layer, kept objects); keep['rotate'] is the layer count."""
     import ctypes
     import torch
     from dkv import _lib
@@ -232,22 +237,32 @@ def attention_setup(past, rotate, bits, nq=64, segments=None, seed=0, precision=
     cache.select(16)
     for layer in range(rotate):
         cache.append(kn, vn, layer)
-    out = torch.empty((1, nq, Q_HEADS, 64), dtype=torch.bfloat16, device=dev)
+    out = [torch.empty((1, nq, Q_HEADS, 64), dtype=torch.bfloat16, device=dev) for _ in range(streams)]
     lib = _lib.load()
-    args = [cache.attend_args(q, kn, vn, layer, past, out, segments, path=path, splits=splits)
+    args = [cache.attend_args(q, kn, vn, layer, past, out[layer % streams], segments, path=path, splits=splits)
             for layer in range(rotate)]
     need = lib.dkv_attend_workspace_bytes(ctypes.byref(args[0]))
-    ws = torch.zeros(max(need, 16), dtype=torch.uint8, device=dev)
-    for a in args:
-        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    ws = [torch.zeros(max(need, 16), dtype=torch.uint8, device=dev) for _ in range(streams)]
+    for i, a in enumerate(args):
+        a.workspace, a.workspace_bytes = ws[i % streams].data_ptr(), ws[i % streams].numel()
     refs = [ctypes.byref(a) for a in args]
+    forks = [torch.cuda.Stream() for _ in range(streams)] if streams > 1 else []
 
     def launch_all():
-        stream = _lib.stream_handle(dev)
-        for r in refs:
-            rc = lib.dkv_attend(r, stream)
+        if not forks:
+            stream = _lib.stream_handle(dev)
+            handles = [stream]
+        else:
+            main = torch.cuda.current_stream()
+            for f in forks:
+                f.wait_stream(main)
+            handles = [ctypes.c_void_p(f.cuda_stream) for f in forks]
+        for i, r in enumerate(refs):
+            rc = lib.dkv_attend(r, handles[i % len(handles)])
             if rc:
                 _lib.check(rc, 'dkv_attend')
+        for f in forks:
+            main.wait_stream(f)
     side = torch.cuda.Stream()
     with torch.cuda.stream(side):
         launch_all()
@@ -258,7 +273,7 @@ def attention_setup(past, rotate, bits, nq=64, segments=None, seed=0, precision=
     torch.cuda.synchronize()
     hist_bytes = history_bytes(bits, lengths)
     chunk_bytes = (Q_HEADS * nq * 64 * 2) * 2 + HEADS * nq * 64 * 2 * 2  # q + out, k_new + v_new
-    keep = dict(cache=cache, keep=(hk, hv, q, kn, vn, out, ws, args), graph=graph, rotate=rotate,
+    keep = dict(cache=cache, keep=(hk, hv, q, kn, vn, out, ws, args, forks), graph=graph, rotate=rotate,
                 rotation_bytes=rotate * hist_bytes)
     return graph.replay, hist_bytes + chunk_bytes, keep
 
@@ -330,6 +345,40 @@ def bench_reference_micro():
                   f'(reference, RTX 5070 Laptop: {ref:.4f} ms), {graph_us:.2f} us per call from a graph',
                   flush=True)
             del graph, cache
+    return out
+
+
+def bench_throughput(steps, warmup, rotate, streams=8):
+    """Independent attention launches in flight together: the rotation's layers dealt round-robin
+    to `streams` streams inside one graph (as independent requests, or the pipelined frames of the
+    decoder, overlap on the GPU), us per layer = graph time / layers. Chunks run the split count
+    pipelined frames use (a quarter of the latency plan's cap: fewer, longer workgroups); decode
+    steps the library's default. Measured with bf16 precision."""
+    from dkv.workloads import bit_schedule, candidate_lengths
+    past = 8128
+    mixed = bit_schedule(past, (past + TILE - 1) // TILE)
+    lengths = candidate_lengths(0, 4)
+    bounds = [0]
+    for n in lengths:
+        bounds.append(bounds[-1] + n)
+    cases = [('frame_chunk_past_8128', past, 64, mixed, None, attention_flops(past, [64]), 12),
+             ('decode_past_8128_nq_1', past, 1, mixed, None, attention_flops(past, [1]), 0),
+             ('candidates_4bit', 6144, bounds[-1], [4] * 96, bounds, attention_flops(6144, lengths), 12),
+             ('candidates_8bit', 6144, bounds[-1], [8] * 96, bounds, attention_flops(6144, lengths), 12)]
+    out = {}
+    for name, p, nq, bits, segs, flops, splits in cases:
+        replay, nbytes, keep = attention_setup(p, rotate, bits, nq=nq, segments=segs, seed=p + nq, splits=splits,
+                                               streams=streams)
+        ms = time_launches(replay, max(1, steps // 10), max(1, warmup // 10)) / keep['rotate']
+        layers = keep['rotate']
+        del keep, replay
+        out[name] = dict(streams=streams, splits=splits or 'default', rotation_layers=layers,
+                         us_per_layer=ms * 1e3, gbs=nbytes / (ms * 1e-3) / 1e9,
+                         hbm_frac=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                         tflops=flops / (ms * 1e-3) / 1e12,
+                         mfma_frac=flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS)
+        print(f"# throughput {name} ({streams} streams, splits {splits or 'default'}): {ms * 1e3:.2f} us/layer, "
+              f"{out[name]['gbs']:.0f} GB/s, {out[name]['tflops']:.1f} TFLOP/s", flush=True)
     return out
 
 
@@ -641,6 +690,8 @@ def main():
                       f"{r['tflops']:.1f} TFLOP/s", flush=True)
     if args.only in ('ref', 'all'):
         res['reference_micro'] = bench_reference_micro()
+    if args.only in ('tput', 'all'):
+        res['throughput'] = bench_throughput(args.steps, args.warmup, args.rotate)
     cpu = None if args.no_cpu else cpu_baselines()
     p = res.get('pack')
     line = dict(
@@ -678,6 +729,12 @@ def main():
             workload='the reference\'s attention microbenchmark: 3 KV / 9 Q heads, 78-token chunk, uniform '
                      '16-bit or 4-bit history, ms per attend() call over 40 eager calls; reference times from '
                      'an RTX 5070 Laptop GPU (other hardware)', **res['reference_micro'])
+    if 'throughput' in res:
+        line['attention_throughput'] = dict(
+            workload='independent attention launches over 8 streams in one graph (requests or pipelined '
+                     'frames in flight together), bf16 precision; us per layer = graph time / layers',
+            **{k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in r.items()}
+               for k, r in res['throughput'].items()})
     if 'e2e' in res:
         line['e2e'] = res['e2e']
     if cpu:
