@@ -74,6 +74,41 @@ __device__ __forceinline__ Unit get_unit(const dkv_attn_args& a, const Hist& hs,
   return un;
 }
 
+// History unit of KV head h from its tile descriptor's four dwords (offset low and high,
+// token_start, rows | bits << 16).
+__device__ __forceinline__ Unit history_unit(const dkv_attn_args& a, const Hist& hs, uint32_t w0, uint32_t w1,
+                                             uint32_t w2, uint32_t w3, int h) {
+  Unit un;
+  un.chunk = false;
+  un.first = (int)w2;
+  un.rows = (int)(w3 & 0xffffu);
+  un.bits = (int)((w3 >> 16) & 0xffu);
+  un.valid = min(un.rows, hs.past - un.first);
+  const int64_t sb = subblock_bytes(un.rows, un.bits);
+  const uint8_t* base = static_cast<const uint8_t*>(a.arena) + (int64_t)((uint64_t)w1 << 32 | w0);
+  un.ksub = base + ((int64_t)(a.layer * 2 + 0) * a.heads + h) * sb;
+  un.vsub = base + ((int64_t)(a.layer * 2 + 1) * a.heads + h) * sb;
+  return un;
+}
+
+// Tile descriptors carried in a launch's argument block (dkv_attn_args.tiles_host): a kernel that
+// takes them has this as its first parameter, so it starts the kernarg segment, and reads
+// descriptor u with one scalar load beside the arguments instead of waiting on the device table.
+struct ArgTiles {
+  dkv_tile t[DKV_ARG_TILES];
+};
+typedef const __attribute__((address_space(4))) uint32_t* kernarg_u32_ptr;
+__device__ __forceinline__ uint4 arg_tile(int u) {
+  const kernarg_u32_ptr p = (kernarg_u32_ptr)__builtin_amdgcn_kernarg_segment_ptr() + 4 * u;
+  return make_uint4(p[0], p[1], p[2], p[3]);
+}
+// Host: whether a launch carries its descriptors (at.t[0, n_tiles) filled from tiles_host).
+inline bool fill_arg_tiles(const dkv_attn_args& a, ArgTiles& at) {
+  if (!a.tiles_host || a.step || a.n_tiles <= 0 || a.n_tiles > DKV_ARG_TILES) return false;
+  for (int i = 0; i < a.n_tiles; ++i) at.t[i] = a.tiles_host[i];
+  return true;
+}
+
 // The default split count of a history of `units` units: at most `cap` splits
 // (the count that keeps every workgroup resident), each of at most
 // ceil(units / cap) units, and no more splits than that needs. So the

@@ -163,42 +163,29 @@ __device__ __forceinline__ void raw_load(const dkv_attn_args& a, const Unit& un,
   }
 }
 
-// Unit u = u0 + rel of a workgroup's range. The first 64 history tiles of the
-// range come from `win`, the descriptors every wave loaded with one vector load
-// at kernel start (lane i holds unit u0 + i), so the unit walk never waits on a
-// scalar load; later tiles fall back to reading the table.
+// Unit u = u0 + rel of a workgroup's range. With `arg_tiles` the history
+// descriptors come from the launch's argument block (one scalar load each).
+// Otherwise the first 64 history tiles of the range come from `win`, the
+// descriptors every wave loaded with one vector load at kernel start (lane i
+// holds unit u0 + i), so the unit walk never waits on a scalar load; later
+// tiles fall back to reading the table.
 __device__ __forceinline__ Unit unit_at(const dkv_attn_args& a, const Hist& hs, int u, int rel, int h,
-                                        const uint4& win) {
+                                        const uint4& win, bool arg_tiles) {
   if (u >= hs.n_tiles) return get_unit(a, hs, u, h);
-  Unit un;
-  uint32_t w0, w1, w2, w3;
-  if (rel < 64) {
-    w0 = (uint32_t)__builtin_amdgcn_readlane((int)win.x, rel);
-    w1 = (uint32_t)__builtin_amdgcn_readlane((int)win.y, rel);
-    w2 = (uint32_t)__builtin_amdgcn_readlane((int)win.z, rel);
-    w3 = (uint32_t)__builtin_amdgcn_readlane((int)win.w, rel);
-  } else {
-    // past the window: the whole descriptor in one 16-byte load (not four narrow ones, whose
-    // destination registers would make every iteration wait on the loads in flight)
-    const uint4 d = *reinterpret_cast<const uint4*>(a.tiles + u);
-    w0 = __builtin_amdgcn_readfirstlane(d.x);
-    w1 = __builtin_amdgcn_readfirstlane(d.y);
-    w2 = __builtin_amdgcn_readfirstlane(d.z);
-    w3 = __builtin_amdgcn_readfirstlane(d.w);
+  if (arg_tiles) {
+    const uint4 d = arg_tile(u);
+    return history_unit(a, hs, d.x, d.y, d.z, d.w, h);
   }
-  const int64_t off = (int64_t)((uint64_t)w1 << 32 | w0);
-  const int tok = (int)w2;
-  const int rows = (int)(w3 & 0xffffu), bits = (int)((w3 >> 16) & 0xffu);
-  un.chunk = false;
-  un.first = tok;
-  un.valid = min(rows, hs.past - tok);
-  un.bits = bits;
-  un.rows = rows;
-  const int64_t sb = subblock_bytes(rows, bits);
-  const uint8_t* base = static_cast<const uint8_t*>(a.arena) + off;
-  un.ksub = base + ((int64_t)(a.layer * 2 + 0) * a.heads + h) * sb;
-  un.vsub = base + ((int64_t)(a.layer * 2 + 1) * a.heads + h) * sb;
-  return un;
+  if (rel < 64)
+    return history_unit(a, hs, (uint32_t)__builtin_amdgcn_readlane((int)win.x, rel),
+                        (uint32_t)__builtin_amdgcn_readlane((int)win.y, rel),
+                        (uint32_t)__builtin_amdgcn_readlane((int)win.z, rel),
+                        (uint32_t)__builtin_amdgcn_readlane((int)win.w, rel), h);
+  // past the window: the whole descriptor in one 16-byte load (not four narrow ones, whose
+  // destination registers would make every iteration wait on the loads in flight)
+  const uint4 d = *reinterpret_cast<const uint4*>(a.tiles + u);
+  return history_unit(a, hs, __builtin_amdgcn_readfirstlane(d.x), __builtin_amdgcn_readfirstlane(d.y),
+                      __builtin_amdgcn_readfirstlane(d.z), __builtin_amdgcn_readfirstlane(d.w), h);
 }
 
 // NBW = 16-row query blocks each wave computes (1..2). A wave whose first
@@ -213,8 +200,8 @@ static __device__ uint64_t tl_mfma[TL_SLOTS * TL_EVENTS];
 
 template <int PREC, int NBW>
 __global__ void __launch_bounds__(MF_THREADS)
-attn_mfma_kernel(dkv_attn_args a, int units, int splits, int cap, int rpg, float* __restrict__ part_o,
-                 float2* __restrict__ part_ml) {
+attn_mfma_kernel(ArgTiles, dkv_attn_args a, int units, int splits, int cap, int rpg, int arg_tiles,
+                 float* __restrict__ part_o, float2* __restrict__ part_ml) {
   // LDS: two raw stages of (K, V) sub-blocks and two sets of bf16 tiles
   // (K, V^T, and for PREC 1 their lo parts). After the last unit the same
   // bytes hold the key-group merge (O rows, then (max, sum) pairs).
@@ -482,12 +469,13 @@ attn_mfma_kernel(dkv_attn_args a, int units, int splits, int cap, int rpg, float
   // So one wave's dequantization overlaps another's MFMAs, and each unit's
   // HBM latency hides behind a full iteration.
   const int n = u1 - u0;
+  const bool in_args = arg_tiles != 0;  // descriptors in the argument block
   uint4 win = make_uint4(0, 0, 0, 0);
-  if (u0 + lane < min(u1, hs.n_tiles)) win = *reinterpret_cast<const uint4*>(a.tiles + u0 + lane);
+  if (!in_args && u0 + lane < min(u1, hs.n_tiles)) win = *reinterpret_cast<const uint4*>(a.tiles + u0 + lane);
   // Wait for the window here, on every path (unit 0 reads it next anyway): a wait the compiler
   // cannot place before the loop lands inside it, where it also waits for the prefetches in flight.
   asm volatile("" ::"v"(win.x), "v"(win.y), "v"(win.z), "v"(win.w));
-  auto unit = [&](int rel) { return unit_at(a, hs, u0 + rel, rel, h, win); };
+  auto unit = [&](int rel) { return unit_at(a, hs, u0 + rel, rel, h, win, in_args); };
   auto stage = [&](int st, const uint4& wk, const uint4& wv) {
     if (t >= MF_LOADERS) return;  // a raw sub-block is at most MF_LOADERS pieces of 16 bytes
     *reinterpret_cast<uint4*>(raw_buf(st, 0) + padded(16 * t)) = wk;
@@ -622,12 +610,14 @@ template <int PREC>
 static void launch_prec(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml, hipStream_t s) {
   const dim3 grid(p.splits, a.heads, p.row_groups);
   const int nbw = (p.rows_per_group / 16 + KG_WAVES - 1) / KG_WAVES;  // blocks of the busiest wave (<= 2)
+  ArgTiles at = {};
+  const int kt = fill_arg_tiles(a, at);
   if (nbw >= 2)
-    hipLaunchKernelGGL((attn_mfma_kernel<PREC, 2>), grid, dim3(MF_THREADS), 0, s, a, p.units, p.splits, p.cap,
-                       p.rows_per_group, part_o, part_ml);
+    hipLaunchKernelGGL((attn_mfma_kernel<PREC, 2>), grid, dim3(MF_THREADS), 0, s, at, a, p.units, p.splits, p.cap,
+                       p.rows_per_group, kt, part_o, part_ml);
   else
-    hipLaunchKernelGGL((attn_mfma_kernel<PREC, 1>), grid, dim3(MF_THREADS), 0, s, a, p.units, p.splits, p.cap,
-                       p.rows_per_group, part_o, part_ml);
+    hipLaunchKernelGGL((attn_mfma_kernel<PREC, 1>), grid, dim3(MF_THREADS), 0, s, at, a, p.units, p.splits, p.cap,
+                       p.rows_per_group, kt, part_o, part_ml);
 }
 
 int launch_attn_mfma(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml, hipStream_t s) {

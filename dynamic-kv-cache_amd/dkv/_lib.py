@@ -14,8 +14,9 @@ from . import _build
 
 DKV_EINVAL = -1
 DKV_MAX_CHUNK_SEGS = 16
+DKV_ARG_TILES = 128  # tile descriptors a launch can carry in its argument block (include/dkv.h)
 DKV_NOALLOC_SCRATCH_BYTES = 16 << 20
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class Tile(ctypes.Structure):
@@ -47,7 +48,7 @@ class AttnArgs(ctypes.Structure):
                 ('out_dtype', ctypes.c_int32), ('path', ctypes.c_int32), ('splits', ctypes.c_int32),
                 ('precision', ctypes.c_int32),
                 ('workspace', ctypes.c_void_p), ('workspace_bytes', ctypes.c_int64),
-                ('step', ctypes.c_void_p)]
+                ('step', ctypes.c_void_p), ('tiles_host', ctypes.c_void_p)]
 
 
 class SegmentIO(ctypes.Structure):

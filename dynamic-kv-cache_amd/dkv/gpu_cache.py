@@ -63,6 +63,12 @@ def segment_bytes(rows, bits, layers, heads):
     return full * slab_bytes(TILE, bits, layers, heads) + (slab_bytes(rem, bits, layers, heads) if rem else 0)
 
 
+# dkv_tile (include/dkv.h): 16 bytes per 64-token tile.
+TILE_DTYPE = np.dtype([('offset', '<i8'), ('token_start', '<i4'), ('rows', '<u2'), ('bits', 'u1'),
+                       ('reserved', 'u1')])
+assert TILE_DTYPE.itemsize == 16
+
+
 def worst_case_arena_bytes(tokens, layers, heads):
     """Bytes that hold `tokens` tokens at any mix of widths and segment cuts."""
     # 16-bit rows are the largest (128 B); each partial tile rounds up by < 16 B.
@@ -131,6 +137,10 @@ class GPUCache(_CacheBase):
         self.arena_bytes = int(arena_bytes) if arena_bytes is not None else max(need, 256)
         self.arena = torch.empty(self.arena_bytes, dtype=torch.uint8, device=self.device)
         self.tiles = torch.zeros((max(max_tiles, 1), 16), dtype=torch.uint8, device=self.device)
+        # Host copy of the tile table, entry for entry what the pack launches write to the device
+        # table (write_tile_descriptors): attention calls pass it in the launch's argument block.
+        # Shared by forks, as the device table is.
+        self.tiles_host = np.zeros(self.tiles.shape[0], dtype=TILE_DTYPE)
         self._workspace = None
         self._graph = None  # GraphSteps while launches read their step parameters from the device
         self._fused_args, self._fused_key = None, None  # the argument block _fused_attention() reuses
@@ -154,6 +164,13 @@ class GPUCache(_CacheBase):
         seg = _Segment(start, n, bits, self.arena_used, tile0, frame)
         self.segments.append(seg)
         self.tile_starts.extend(range(start, start + n, TILE))
+        t = np.arange((n + TILE - 1) // TILE)
+        entries = self.tiles_host[tile0:tile0 + len(t)]
+        entries['offset'] = self.arena_used + t * slab_bytes(TILE, bits, self.layers, self.heads)
+        entries['token_start'] = start + t * TILE
+        entries['rows'] = np.minimum(n - t * TILE, TILE)
+        entries['bits'] = bits
+        entries['reserved'] = 0
         self.plan.append((start, start + n, bits, self.host_counts[bits]))
         self.host_counts[bits] += n
         self.arena_used += need
@@ -357,7 +374,7 @@ class GPUCache(_CacheBase):
             a.scale = d ** -0.5
             a.out_tok_stride, a.out_head_stride = q_heads * d, d
         a.q, a.k_new, a.v_new, a.out = qkv_out, kp, vp, out
-        a.arena, a.tiles = self.arena.data_ptr(), self.tiles.data_ptr()
+        a.arena, a.tiles, a.tiles_host = self.arena.data_ptr(), self.tiles.data_ptr(), self.tiles_host.ctypes.data
         a.n_tiles, a.past, a.layer = self._tiles_before(past), past, layer
         a.precision = PRECISIONS[self.precision]
         if q_heads // H * n > SHORT_ROWS:
@@ -423,6 +440,7 @@ class GPUCache(_CacheBase):
         a.v_new, a.vn_head_stride, a.vn_tok_stride = v.data_ptr(), v.stride(1), v.stride(2)
         a.arena, a.tiles = self.arena.data_ptr(), self.tiles.data_ptr()
         a.n_tiles, a.past = self._tiles_before(past), past
+        a.tiles_host = self.tiles_host.ctypes.data
         a.layer, a.layers, a.heads, a.q_heads, a.nq = layer, self.layers, self.heads, q.shape[1], nq
         if segments:
             if len(segments) - 1 > _lib.DKV_MAX_CHUNK_SEGS:  # bounds [0, b1, ..., nq]: one more than segments

@@ -30,10 +30,11 @@
 extern "C" {
 #endif
 
-#define DKV_ABI_VERSION 2
+#define DKV_ABI_VERSION 3
 #define DKV_HEAD_DIM 64
 #define DKV_TILE_TOKENS 64
 #define DKV_MAX_CHUNK_SEGS 16
+#define DKV_ARG_TILES 128 /* most tile descriptors a launch carries in its argument block */
 #define DKV_EINVAL (-1)
 
 /* One 64-token tile of the arena. The cache keeps these in token order in a
@@ -99,6 +100,11 @@ typedef struct dkv_attn_args {
                             for launches recorded once in a HIP graph and replayed as the
                             history grows. `past` and `n_tiles` above then bound the launch
                             (grid, workspace) and the device pair must stay within them. */
+  const dkv_tile* tiles_host; /* NULL, or a HOST copy of tiles[0, n_tiles), equal to the device
+                            table. For a launch without `step` and n_tiles <= DKV_ARG_TILES the
+                            frame-chunk kernel then takes the descriptors from its argument block
+                            (read beside the arguments) instead of waiting on the device table
+                            before its first history loads; otherwise it is ignored. */
 } dkv_attn_args;
 
 /* One segment of the arena in the reference's CPU-cache layout: what

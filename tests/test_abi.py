@@ -26,7 +26,7 @@ def test_every_declared_symbol_is_exported():
     for name in names:
         assert hasattr(lib, name), name
     assert {n for n, _, _ in _lib.SIGNATURES} == set(names)
-    assert lib.dkv_version() == 2
+    assert lib.dkv_version() == _lib.ABI_VERSION == 3
 
 
 STRUCT_PROBE = r'''
@@ -42,6 +42,7 @@ int main(void) {
   printf("DKV_MAX_CHUNK_SEGS const %d\n", DKV_MAX_CHUNK_SEGS);
   printf("DKV_NOALLOC_SCRATCH_BYTES const %d\n", DKV_NOALLOC_SCRATCH_BYTES);
   printf("DKV_ABI_VERSION const %d\n", DKV_ABI_VERSION);
+  printf("DKV_ARG_TILES const %d\n", DKV_ARG_TILES);
   %FIELDS%
   return 0;
 }
@@ -61,7 +62,8 @@ def test_struct_layout_matches_header(tmp_path, cls, cname):
     assert sizes[cname] == ctypes.sizeof(cls)
     consts = {l.split()[0]: int(l.split()[2]) for l in lines if ' const ' in l}
     assert consts == dict(DKV_MAX_CHUNK_SEGS=_lib.DKV_MAX_CHUNK_SEGS,
-                          DKV_NOALLOC_SCRATCH_BYTES=_lib.DKV_NOALLOC_SCRATCH_BYTES, DKV_ABI_VERSION=_lib.ABI_VERSION)
+                          DKV_NOALLOC_SCRATCH_BYTES=_lib.DKV_NOALLOC_SCRATCH_BYTES, DKV_ABI_VERSION=_lib.ABI_VERSION,
+                          DKV_ARG_TILES=_lib.DKV_ARG_TILES)
     for line in lines:
         parts = line.split()
         if len(parts) == 3 and parts[0] == cname and parts[1] != 'size':
