@@ -652,8 +652,6 @@ def main():
         # same process (914 vs 1148 frames/s at 96 frames on one box); the other legs' numbers do
         # not depend on running after it
         res['e2e'] = bench_e2e()
-    if args.only in ('tput', 'all'):
-        res['throughput'] = bench_throughput(args.steps, args.warmup, args.rotate)
     if args.only in ('pack', 'all'):
         res['pack'] = bench_pack(args.steps, args.warmup)
         print(f"# pack: {res['pack']['ms'] * 1e3:.1f} us/launch, {res['pack']['gbs']:.0f} GB/s", flush=True)
@@ -692,6 +690,9 @@ def main():
                       f"{r['tflops']:.1f} TFLOP/s", flush=True)
     if args.only in ('ref', 'all'):
         res['reference_micro'] = bench_reference_micro()
+    if args.only in ('tput', 'all'):
+        # last: its multi-stream replays vary more from run to run than the single-stream legs
+        res['throughput'] = bench_throughput(args.steps, args.warmup, args.rotate)
     cpu = None if args.no_cpu else cpu_baselines()
     p = res.get('pack')
     line = dict(
