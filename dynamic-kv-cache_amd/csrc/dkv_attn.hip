@@ -473,6 +473,25 @@ static int check_args(const dkv_attn_args& a) {
     set_error("dkv_attend: out must be 16-byte aligned with strides that are multiples of 4 elements");
     return DKV_EINVAL;
   }
+  if (a.tiles_host && !a.step && a.n_tiles > 0 && a.n_tiles <= DKV_ARG_TILES) {
+    // The host copy goes into the frame-chunk kernel's argument block as given: its tiles must be
+    // well formed and cover [0, past) in token order, as the cache's table does.
+    int next = 0;
+    for (int i = 0; i < a.n_tiles; ++i) {
+      const dkv_tile& t = a.tiles_host[i];
+      if ((t.bits != 4 && t.bits != 8 && t.bits != 16) || t.rows < 1 || t.rows > TILE || t.offset < 0 ||
+          t.token_start != next) {
+        set_error("dkv_attend: tiles_host[%d] (token_start %d, rows %d, bits %d) is not the tile after "
+                  "token %d", i, t.token_start, (int)t.rows, (int)t.bits, next);
+        return DKV_EINVAL;
+      }
+      next += t.rows;
+    }
+    if (next < a.past || a.tiles_host[a.n_tiles - 1].token_start >= a.past) {
+      set_error("dkv_attend: tiles_host's %d tiles do not end at past %d", a.n_tiles, a.past);
+      return DKV_EINVAL;
+    }
+  }
   return 0;
 }
 

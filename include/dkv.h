@@ -104,7 +104,9 @@ typedef struct dkv_attn_args {
                             table. For a launch without `step` and n_tiles <= DKV_ARG_TILES the
                             frame-chunk kernel then takes the descriptors from its argument block
                             (read beside the arguments) instead of waiting on the device table
-                            before its first history loads; otherwise it is ignored. */
+                            before its first history loads; otherwise it is ignored. A copy whose
+                            tiles are not well formed or do not cover [0, past) in token order is
+                            refused (DKV_EINVAL). */
 } dkv_attn_args;
 
 /* One segment of the arena in the reference's CPU-cache layout: what

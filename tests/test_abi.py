@@ -152,6 +152,45 @@ def test_attend_rejects_bad_segments():
     assert lib.dkv_attend(ctypes.byref(a), None) == _lib.DKV_EINVAL
 
 
+def host_tiles(rows):
+    """A dkv_tile array of consecutive tiles of the given row counts (8-bit, packed one after
+    another)."""
+    arr = (_lib.Tile * len(rows))()
+    start = 0
+    for i, r in enumerate(rows):
+        arr[i].offset, arr[i].token_start, arr[i].rows, arr[i].bits = 4096 * i, start, r, 8
+        start += r
+    return arr
+
+
+@pytest.mark.parametrize('change', [None, 'bits', 'rows', 'gap', 'short', 'step'])
+def test_attend_checks_the_host_tile_copy(change):
+    """tiles_host (the descriptors the frame-chunk kernel then takes from its argument block) must
+    be well formed and cover [0, past) in token order; a bad copy is refused before any launch.
+    With a device step pair the copy is not used and not checked."""
+    lib = _lib.load()
+    arr = host_tiles([64, 64, 30])
+    a = attn(past=158, n_tiles=3, arena=4096, tiles=4096)
+    if change == 'bits':
+        arr[1].bits = 5
+    elif change == 'rows':
+        arr[2].rows = 65
+    elif change == 'gap':
+        arr[2].token_start = 129
+    elif change == 'short':
+        a.past = 159  # the tiles end at 158
+    elif change == 'step':
+        arr[1].bits = 5
+        a.step = 4096
+    a.tiles_host = ctypes.addressof(arr)
+    assert lib.dkv_attend(ctypes.byref(a), None) == _lib.DKV_EINVAL
+    msg = lib.dkv_last_error().decode()
+    if change in (None, 'step'):
+        assert 'workspace' in msg  # past the tile checks, at the next one
+    else:
+        assert 'tiles_host' in msg, msg
+
+
 def test_attend_demands_workspace_when_split():
     lib = _lib.load()
     a = attn(past=4096, n_tiles=64, arena=4096, tiles=4096)
