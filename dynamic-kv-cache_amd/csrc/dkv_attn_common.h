@@ -97,6 +97,11 @@ __device__ __forceinline__ Unit history_unit(const dkv_attn_args& a, const Hist&
 struct ArgTiles {
   dkv_tile t[DKV_ARG_TILES];
 };
+// The first parameter of a kernel variant that does not carry them: 4 bytes, not 2 KB (a larger
+// argument block slows every launch that has to fetch it, including those reading the table).
+struct NoArgTiles {
+  int unused;
+};
 typedef const __attribute__((address_space(4))) uint32_t* kernarg_u32_ptr;
 __device__ __forceinline__ uint4 arg_tile(int u) {
   const kernarg_u32_ptr p = (kernarg_u32_ptr)__builtin_amdgcn_kernarg_segment_ptr() + 4 * u;
@@ -106,6 +111,7 @@ __device__ __forceinline__ uint4 arg_tile(int u) {
 inline bool fill_arg_tiles(const dkv_attn_args& a, ArgTiles& at) {
   if (!a.tiles_host || a.step || a.n_tiles <= 0 || a.n_tiles > DKV_ARG_TILES) return false;
   for (int i = 0; i < a.n_tiles; ++i) at.t[i] = a.tiles_host[i];
+  for (int i = a.n_tiles; i < DKV_ARG_TILES; ++i) at.t[i] = dkv_tile{};  // unused, but defined bytes
   return true;
 }
 

@@ -49,6 +49,7 @@
 //      O = P_hi V_hi + P_hi V_lo + P_lo V_hi; the lo terms are skipped for
 //      bf16 units, where they are exactly zero.
 #include "dkv_attn_common.h"
+#include <type_traits>
 
 namespace dkv {
 
@@ -198,10 +199,12 @@ __device__ __forceinline__ Unit unit_at(const dkv_attn_args& a, const Hist& hs, 
 static __device__ uint64_t tl_mfma[TL_SLOTS * TL_EVENTS];
 #endif
 
-template <int PREC, int NBW>
+// ARGT: the history's tile descriptors come in the argument block (first parameter ArgTiles)
+// rather than from the device table (first parameter NoArgTiles).
+template <int PREC, int NBW, bool ARGT>
 __global__ void __launch_bounds__(MF_THREADS)
-attn_mfma_kernel(ArgTiles, dkv_attn_args a, int units, int splits, int cap, int rpg, int arg_tiles,
-                 float* __restrict__ part_o, float2* __restrict__ part_ml) {
+attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dkv_attn_args a, int units,
+                 int splits, int cap, int rpg, float* __restrict__ part_o, float2* __restrict__ part_ml) {
   // LDS: two raw stages of (K, V) sub-blocks and two sets of bf16 tiles
   // (K, V^T, and for PREC 1 their lo parts). After the last unit the same
   // bytes hold the key-group merge (O rows, then (max, sum) pairs).
@@ -469,7 +472,7 @@ attn_mfma_kernel(ArgTiles, dkv_attn_args a, int units, int splits, int cap, int 
   // So one wave's dequantization overlaps another's MFMAs, and each unit's
   // HBM latency hides behind a full iteration.
   const int n = u1 - u0;
-  const bool in_args = arg_tiles != 0;  // descriptors in the argument block
+  constexpr bool in_args = ARGT;  // descriptors in the argument block
   uint4 win = make_uint4(0, 0, 0, 0);
   if (!in_args && u0 + lane < min(u1, hs.n_tiles)) win = *reinterpret_cast<const uint4*>(a.tiles + u0 + lane);
   // Wait for the window here, on every path (unit 0 reads it next anyway): a wait the compiler
@@ -610,14 +613,23 @@ template <int PREC>
 static void launch_prec(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml, hipStream_t s) {
   const dim3 grid(p.splits, a.heads, p.row_groups);
   const int nbw = (p.rows_per_group / 16 + KG_WAVES - 1) / KG_WAVES;  // blocks of the busiest wave (<= 2)
-  ArgTiles at = {};
-  const int kt = fill_arg_tiles(a, at);
-  if (nbw >= 2)
-    hipLaunchKernelGGL((attn_mfma_kernel<PREC, 2>), grid, dim3(MF_THREADS), 0, s, at, a, p.units, p.splits, p.cap,
-                       p.rows_per_group, kt, part_o, part_ml);
-  else
-    hipLaunchKernelGGL((attn_mfma_kernel<PREC, 1>), grid, dim3(MF_THREADS), 0, s, at, a, p.units, p.splits, p.cap,
-                       p.rows_per_group, kt, part_o, part_ml);
+  ArgTiles at;
+  const NoArgTiles none = {0};
+  const int rpg = p.rows_per_group;
+  if (fill_arg_tiles(a, at)) {
+    if (nbw >= 2)
+      hipLaunchKernelGGL((attn_mfma_kernel<PREC, 2, true>), grid, dim3(MF_THREADS), 0, s, at, a, p.units, p.splits,
+                         p.cap, rpg, part_o, part_ml);
+    else
+      hipLaunchKernelGGL((attn_mfma_kernel<PREC, 1, true>), grid, dim3(MF_THREADS), 0, s, at, a, p.units, p.splits,
+                         p.cap, rpg, part_o, part_ml);
+  } else if (nbw >= 2) {
+    hipLaunchKernelGGL((attn_mfma_kernel<PREC, 2, false>), grid, dim3(MF_THREADS), 0, s, none, a, p.units, p.splits,
+                       p.cap, rpg, part_o, part_ml);
+  } else {
+    hipLaunchKernelGGL((attn_mfma_kernel<PREC, 1, false>), grid, dim3(MF_THREADS), 0, s, none, a, p.units, p.splits,
+                       p.cap, rpg, part_o, part_ml);
+  }
 }
 
 int launch_attn_mfma(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml, hipStream_t s) {
