@@ -141,6 +141,7 @@ class GPUCache(_CacheBase):
         # table (write_tile_descriptors): attention calls pass it in the launch's argument block.
         # Shared by forks, as the device table is.
         self.tiles_host = np.zeros(self.tiles.shape[0], dtype=TILE_DTYPE)
+        self._tiles_host_ptr = self.tiles_host.ctypes.data  # fixed: the array is never replaced
         self._workspace = None
         self._graph = None  # GraphSteps while launches read their step parameters from the device
         self._fused_args, self._fused_key = None, None  # the argument block _fused_attention() reuses
@@ -374,7 +375,7 @@ class GPUCache(_CacheBase):
             a.scale = d ** -0.5
             a.out_tok_stride, a.out_head_stride = q_heads * d, d
         a.q, a.k_new, a.v_new, a.out = qkv_out, kp, vp, out
-        a.arena, a.tiles, a.tiles_host = self.arena.data_ptr(), self.tiles.data_ptr(), self.tiles_host.ctypes.data
+        a.arena, a.tiles, a.tiles_host = self.arena.data_ptr(), self.tiles.data_ptr(), self._tiles_host_ptr
         a.n_tiles, a.past, a.layer = self._tiles_before(past), past, layer
         a.precision = PRECISIONS[self.precision]
         if q_heads // H * n > SHORT_ROWS:
@@ -440,7 +441,7 @@ class GPUCache(_CacheBase):
         a.v_new, a.vn_head_stride, a.vn_tok_stride = v.data_ptr(), v.stride(1), v.stride(2)
         a.arena, a.tiles = self.arena.data_ptr(), self.tiles.data_ptr()
         a.n_tiles, a.past = self._tiles_before(past), past
-        a.tiles_host = self.tiles_host.ctypes.data
+        a.tiles_host = self._tiles_host_ptr
         a.layer, a.layers, a.heads, a.q_heads, a.nq = layer, self.layers, self.heads, q.shape[1], nq
         if segments:
             if len(segments) - 1 > _lib.DKV_MAX_CHUNK_SEGS:  # bounds [0, b1, ..., nq]: one more than segments
