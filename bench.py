@@ -48,6 +48,8 @@ def parse():
     p.add_argument('--timeline', choices=['short', 'mfma'],
                    help='instead of the benchmark: workgroup timelines of one attention launch of that kernel, '
                         'from the timeline build (python dynamic-kv-cache_amd/dkv/_build.py --timeline)')
+    p.add_argument('--decode-path', choices=['auto', 'short', 'mfma', 'vector'], default='auto',
+                   help='kernel of the decode-step legs (auto: the library\'s choice)')
     p.add_argument('--past', type=int, default=8128, help='--timeline: history tokens')
     p.add_argument('--nq', type=int, default=0, help='--timeline: chunk tokens (default 1 short, 64 mfma)')
     return p.parse_args()
@@ -389,11 +391,12 @@ def attainable(nbytes, flops, ms):
     return dict(roofline_us=t * 1e6, attainable_frac=t / (ms * 1e-3))
 
 
-def bench_decode(past, nq, steps, warmup, rotate, precision='bf16'):
+def bench_decode(past, nq, steps, warmup, rotate, precision='bf16', path='auto'):
     """A short chunk (nq = 1: one decode token) over a mixed history; us per layer."""
     from dkv.workloads import bit_schedule
     bits = bit_schedule(past, (past + TILE - 1) // TILE)
-    replay, nbytes, keep = attention_setup(past, rotate, bits, nq=nq, seed=past + nq, precision=precision)
+    replay, nbytes, keep = attention_setup(past, rotate, bits, nq=nq, seed=past + nq, precision=precision,
+                                           path=path)
     ms = time_launches(replay, max(1, steps // 10), max(1, warmup // 10)) / keep['rotate']
     flops = attention_flops(past, [nq])
     rot = dict(rotation_layers=keep['rotate'], rotation_mb=round(keep['rotation_bytes'] / 1e6, 1))
@@ -676,7 +679,7 @@ def main():
         res['decode'] = {}
         for prec in ('bf16', 'fp32'):
             for nq in (1, 4):
-                r = bench_decode(8128, nq, args.steps, args.warmup, args.rotate, prec)
+                r = bench_decode(8128, nq, args.steps, args.warmup, args.rotate, prec, args.decode_path)
                 res['decode'][f'{prec}_past_8128_nq_{nq}'] = r
                 print(f"# decode {prec} past=8128 nq={nq}: {r['us_per_layer']:.2f} us/layer, {r['gbs']:.0f} GB/s",
                       flush=True)

@@ -469,8 +469,8 @@ class GPUCache(_CacheBase):
 
         `segments` (optional) lists chunk boundaries [0, b1, ..., nq] for a block-diagonal batch of
         independent continuations that share the history, e.g. QA candidates. `path` is 'auto' (the
-        short-chunk kernel when q_heads / heads * n <= 16, e.g. decode steps, else the frame-chunk
-        MFMA kernel), 'short', 'mfma' or 'vector'; `precision` overrides the cache's 'bf16' / 'fp32'
+        frame-chunk MFMA kernel, the fastest for every chunk length, decode steps included),
+        'mfma', 'short' (the short-chunk kernel, at most 16 query rows per KV head) or 'vector'; `precision` overrides the cache's 'bf16' / 'fp32'
         setting for this call.
         """
         if precision is not None and precision not in PRECISIONS:

@@ -89,7 +89,8 @@ typedef struct dkv_attn_args {
   void* out;             /* [nq, q_heads, 64] with the strides below */
   int64_t out_tok_stride, out_head_stride;
   int32_t out_dtype;     /* 0 = bf16, 1 = fp32 */
-  int32_t path;          /* 0 = auto (short chunk when q_heads / heads * nq <= 16, else MFMA),
+  int32_t path;          /* 0 = auto (the MFMA frame-chunk kernel, the fastest measured for every
+                            chunk length, decode steps included),
                             1 = vector, 2 = MFMA (frame chunks), 3 = short chunk (decode steps) */
   int32_t splits;        /* 0 = auto; history split count per KV head */
   int32_t precision;     /* 0 = the reference kernel's bf16 rounding of K, V and p

@@ -202,8 +202,9 @@ def test_attend_demands_workspace_when_split():
 
 def test_attend_workspace_matches_the_partial_format():
     """Per split row: 64 fp16 O / sum values + (max, sum) in bf16 precision, 64 fp32 O + (max, sum)
-    in fp32 precision; the short-chunk kernel keeps fp32 rows in both precisions, one split per 4
-    units (64-token tiles plus the chunk) by default."""
+    in fp32 precision; the short-chunk kernel (path 3) keeps fp32 rows in both precisions, one
+    split per 4 units (64-token tiles plus the chunk) by default. Auto takes the frame-chunk
+    kernel for decode steps too."""
     lib = _lib.load()
     need = {}
     for precision in (0, 1):
@@ -212,10 +213,12 @@ def test_attend_workspace_matches_the_partial_format():
     rows = need[1] // (64 * 4 + 8)
     assert rows > 0 and need[1] == rows * (64 * 4 + 8) and need[0] == rows * (64 * 2 + 8)
     for precision in (0, 1):
-        a = attn(past=4096, n_tiles=64, arena=4096, tiles=4096, nq=1, precision=precision)
-        assert a.q_heads // a.heads * a.nq <= 16  # auto takes the short-chunk kernel
+        a = attn(past=4096, n_tiles=64, arena=4096, tiles=4096, nq=1, precision=precision, path=3)
         splits = (64 + 1 + 3) // 4
         assert lib.dkv_attend_workspace_bytes(ctypes.byref(a)) == a.heads * splits * 3 * (64 * 4 + 8)
+        auto = attn(past=4096, n_tiles=64, arena=4096, tiles=4096, nq=1, precision=precision)
+        mfma = attn(past=4096, n_tiles=64, arena=4096, tiles=4096, nq=1, precision=precision, path=2)
+        assert lib.dkv_attend_workspace_bytes(ctypes.byref(auto)) == lib.dkv_attend_workspace_bytes(ctypes.byref(mfma))
 
 
 def test_pack_validate_checks_every_job_of_a_host_table():
