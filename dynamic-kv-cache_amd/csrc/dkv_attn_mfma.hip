@@ -468,7 +468,9 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
 
   // Software pipeline, one barrier per unit: iteration i dequantizes unit
   // i+1 into the other tile set, stages unit i+2's raw bytes (loaded during
-  // iteration i-1) and issues unit i+3's loads, then runs unit i's MFMA work.
+  // iteration i-1; with two query blocks per wave unit 2's at kernel start) and
+  // issues unit i+3's loads, then
+  // runs unit i's MFMA work.
   // So one wave's dequantization overlaps another's MFMAs, and each unit's
   // HBM latency hides behind a full iteration.
   const int n = u1 - u0;
@@ -484,9 +486,15 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
     *reinterpret_cast<uint4*>(raw_buf(st, 0) + padded(16 * t)) = wk;
     *reinterpret_cast<uint4*>(raw_buf(st, 1) + padded(16 * t)) = wv;
   };
-  uint4 wk, wv, wk0, wv0;
+  uint4 wk, wv, wk0, wv0, wk2, wv2;
   if (n > 0) raw_load(a, unit(0), h, wk0, wv0);
   if (n > 1) raw_load(a, unit(1), h, wk, wv);  // in flight while unit 0 is staged
+  // With two query blocks per wave (frame chunks, candidate batches) unit 2's loads go out at
+  // once too, not after unit 0 is staged and dequantized (past 1024 11.60 -> 11.37 us, 4096
+  // 13.98 -> 13.83). With one (decode steps), whose units compute little, the larger first
+  // burst delayed unit 0 more than it saved (11.68 -> 11.83 us at past 8128).
+  constexpr bool early2 = NBW == 2;
+  if (early2 && n > 2) raw_load(a, unit(2), h, wk2, wv2);
   if (n > 0) stage(0, wk0, wv0);
   // unit 0's load registers are settled on every path before the loop (the compiler does not
   // tie the two n > 0 tests together and would otherwise wait on them inside the loop, where a
@@ -497,12 +505,15 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
   if (n > 0) dequant(unit(0), 0, 0);
   DKV_TL(tl_mfma, 2);
   if (n > 1) stage(1, wk, wv);
-  if (n > 2) raw_load(a, unit(2), h, wk, wv);
+  if (!early2 && n > 2) raw_load(a, unit(2), h, wk, wv);
   for (int i = 0; i < n; ++i) {
     __syncthreads();
     if (i + 1 < n) dequant(unit(i + 1), (i + 1) & 1, (i + 1) & 1);
     if (i + 2 < n) {
-      stage(i & 1, wk, wv);
+      if (early2 && i == 0)
+        stage(0, wk2, wv2);
+      else
+        stage(i & 1, wk, wv);
       if (i + 3 < n) raw_load(a, unit(i + 3), h, wk, wv);
     }
     compute(unit(i), i & 1);
