@@ -1,7 +1,9 @@
-// Short-chunk path of the fused packed-history attention (gfx950): decode
-// steps and other chunks with at most 16 query rows per KV head (G * nq <= 16,
-// e.g. one to five tokens of a 3-way GQA decoder), where the whole job is to
-// stream the packed history once.
+// Short-chunk path of the fused packed-history attention (gfx950), path 3:
+// decode steps and other chunks with at most 16 query rows per KV head
+// (G * nq <= 16, e.g. one to five tokens of a 3-way GQA decoder), where the
+// whole job is to stream the packed history once. The auto path takes the
+// frame-chunk kernel for these too, which measured faster at every history
+// length; this kernel stays as a second implementation.
 //
 // Work split: two waves own one 64-key unit (a history tile, or the chunk's
 // own native rows), one 32-key half each; a workgroup of 8 waves owns a
