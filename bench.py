@@ -50,6 +50,12 @@ def parse():
                         'from the timeline build (python dynamic-kv-cache_amd/dkv/_build.py --timeline)')
     p.add_argument('--decode-path', choices=['auto', 'short', 'mfma', 'vector'], default='auto',
                    help='kernel of the decode-step legs (auto: the library\'s choice)')
+    p.add_argument('--lib', help='load this build of libdkv instead of the package\'s (e.g. the in-kernel merge '
+                                 'build, dynamic-kv-cache_amd/dkv/_build.py --in-kernel-merge); with --timeline, '
+                                 'its timeline build')
+    p.add_argument('--tl-path', choices=['auto', 'mfma', 'short'],
+                   help='--timeline: the path argument of the timed launches (default: auto for the frame-chunk '
+                        'kernel, short for the short-chunk one)')
     p.add_argument('--past', type=int, default=8128, help='--timeline: history tokens')
     p.add_argument('--nq', type=int, default=0, help='--timeline: chunk tokens (default 1 short, 64 mfma)')
     return p.parse_args()
@@ -483,11 +489,13 @@ TIMELINE_EVENTS = {  # stamp index -> name, in the order printed
     'short': [(0, 'entry'), (5, 'arguments'), (1, 'first descriptor'), (2, 'first K/V'), (3, 'units done'),
               (4, 'workgroup merge')],
     'mfma': [(0, 'entry'), (7, 'arguments'), (1, 'unit 0 staged'), (2, 'unit 0 dequantized'),
-             (3, 'unit 0 computed'), (4, 'all units'), (5, 'key-group merge'), (6, 'stores')],
+             (3, 'unit 0 computed'), (4, 'all units'), (5, 'key-group merge'), (6, 'stores'),
+             (8, 'arrival counted'), (9, 'in-kernel merge')],  # 8, 9: the in-kernel merge build only
 }
+TIMELINE_STAMPS = 10  # stamps per workgroup in the timeline build (TL_EVENTS)
 
 
-def timeline(kind, past, nq, rotate):
+def timeline(kind, past, nq, rotate, path=None):
     """Workgroup timelines of the attention kernel `kind` from the timeline build: lane 0 of each
     workgroup stamps wall_clock64() (100 MHz) at numbered points; after timed graph replays over the
     rotation, the stamps of the last launch (and of its split-merge kernel) are read and each
@@ -503,25 +511,25 @@ def timeline(kind, past, nq, rotate):
     lib = _lib.load()
     nq = nq or (1 if kind == 'short' else 64)
     bits = bit_schedule(past, (past + TILE - 1) // TILE)
-    replay, nbytes, keep = attention_setup(past, rotate, bits, nq=nq, seed=past + nq, path=kind)
+    path = path or ('auto' if kind == 'mfma' else kind)
+    replay, nbytes, keep = attention_setup(past, rotate, bits, nq=nq, seed=past + nq, path=path)
     ms = time_launches(replay, 10, 2) / keep['rotate']
     torch.cuda.synchronize()
 
     def read(name):
         f = getattr(lib, name)
         f.restype, f.argtypes = ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64]
-        stamps = np.zeros((1 << 14) * 8, dtype=np.uint64)
+        stamps = np.zeros((1 << 14) * TIMELINE_STAMPS, dtype=np.uint64)
         _lib.check(f(stamps.ctypes.data, stamps.nbytes), name)
-        t = stamps.reshape(-1, 8).astype(np.int64)
+        t = stamps.reshape(-1, TIMELINE_STAMPS).astype(np.int64)
         return t[t[:, 0] > 0]
     t = read('dkv_timeline_' + kind)
     merge = read('dkv_timeline_combine')
     t0 = t[:, 0].min()
-    print(f'# {kind} kernel, past={past} nq={nq}: {ms * 1e3:.2f} us/layer (timeline build), '
+    print(f'# {kind} kernel (path {path}), past={past} nq={nq}: {ms * 1e3:.2f} us/layer (timeline build), '
           f'{len(t)} workgroups recorded; merge kernel: {len(merge)} workgroups', flush=True)
     events = [(t, e, name) for e, name in TIMELINE_EVENTS[kind]]
-    events += [(merge, e, 'merge ' + name) for e, name in enumerate(['entry', 'arguments', 'partials merged',
-                                                                   'row stored'])]
+    events += [(merge, e, 'merge ' + name) for e, name in ((0, 'entry'), (1, 'arguments'), (3, 'row stored'))]
     for tt, e, name in events:
         col = (tt[:, e][tt[:, e] > 0] - t0) * 10 / 1000.0  # 100 MHz ticks -> us
         if len(col):
@@ -644,8 +652,11 @@ def main():
     if not torch.cuda.is_available():
         print(json.dumps(dict(error='no HIP device visible')), flush=True)
         sys.exit(2)
+    if args.lib:
+        from dkv import _build
+        _build.LIB_PATH = _build.TIMELINE_LIB_PATH = os.path.abspath(args.lib)
     if args.timeline:
-        timeline(args.timeline, args.past, args.nq, args.rotate)
+        timeline(args.timeline, args.past, args.nq, args.rotate, args.tl_path)
         return
     from dkv import _lib
     _lib.load()

@@ -15,6 +15,7 @@
 // value, well under the bf16 output's rounding, at half the partial traffic).
 // Softmax runs in base 2: x = score * scale * log2(e).
 #include "dkv_attn_common.h"
+#include "dkv_merge.h"
 #include <mutex>
 
 namespace dkv {
@@ -239,16 +240,12 @@ attn_vec_kernel(dkv_attn_args a, int units, int splits, int cap, float* __restri
 // layer; candidate batches 15.9 -> 15.7 us).
 //
 #ifdef DKV_TIMELINE
-// events (both merge kernels): 0 entry, 1 arguments arrived, 2 partials merged, 3 row stored
+// events (both merge kernels): 0 entry, 1 arguments arrived, 3 row stored
 static __device__ uint64_t tl_comb[TL_SLOTS * TL_EVENTS];
 #endif
 //
-// Precision-1 merge (unnormalized fp32 O partials, 256 bytes per row): one
-// wave per query row. Lane l = 16 j + c reads 16-byte chunk c (columns
-// 4c + [0, 4)) of split s0 + 4 i + j for i = 0..15, so each load instruction
-// covers 4 splits, and accumulates them weighted by 2^(m_s - M), computed once
-// on lane s and fetched with a shuffle. The 4 lanes of one chunk are summed at
-// the end, and lanes 0..15 store the row.
+// The two merge kernels: one wave per query row of a KV head, the row's arithmetic in
+// merge_row_f32 (precision 1) and merge_row_half (precision 0), dkv_merge.h.
 __global__ void __launch_bounds__(256)
 combine_kernel(dkv_attn_args a, int splits, int cap, int short_plan, const float* __restrict__ part_o,
                const float2* __restrict__ part_ml) {
@@ -257,7 +254,6 @@ combine_kernel(dkv_attn_args a, int splits, int cap, int short_plan, const float
   const int G = a.q_heads / a.heads;
   const int R = G * a.nq;
   const int r = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
   if (r >= R) return;
   int units = a.n_tiles + (a.nq + TILE - 1) / TILE;
   Hist hs;
@@ -265,67 +261,10 @@ combine_kernel(dkv_attn_args a, int splits, int cap, int short_plan, const float
   const int active = short_plan ? short_runtime_plan(a, hs, units, splits) : runtime_plan(a, hs, units, splits, cap);
   if (active <= 1) return;  // one split ran and stored the output itself
   DKV_TL(tl_comb, 1);
-  const int64_t base = (int64_t)h * splits * R + r;
-  const int j = lane >> 4, c = lane & 15;
-  const float4* rows = reinterpret_cast<const float4*>(part_o);  // 16 chunks of 16 bytes per row
-  float M = -INFINITY, L = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int s0 = 0; s0 < active; s0 += 64) {
-    const int cnt = min(64, active - s0);
-    const float2 ml = lane < cnt ? part_ml[base + (int64_t)(s0 + lane) * R] : make_float2(-INFINITY, 0.f);
-    float4 raw[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int sp = 4 * i + j;
-      const u32x4* src = reinterpret_cast<const u32x4*>(rows) + (base + (int64_t)(s0 + sp) * R) * 16 + c;
-      raw[i] = sp < cnt ? __builtin_bit_cast(float4, __builtin_nontemporal_load(src)) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    float bm = ml.x;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) bm = fmaxf(bm, __shfl_xor(bm, o));
-    bm = fmaxf(bm, M);
-    if (bm == -INFINITY) continue;  // wave-uniform: every split so far saw no visible key
-    const float f = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - bm);
-    float lsum = ml.y * f;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o);
-    const float f0 = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - bm);
-    L = fmaf(L, f0, lsum);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) acc[e] *= f0;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float w = __shfl(f, 4 * i + j);  // 0 for splits past cnt
-      acc[0] = fmaf(raw[i].x, w, acc[0]);
-      acc[1] = fmaf(raw[i].y, w, acc[1]);
-      acc[2] = fmaf(raw[i].z, w, acc[2]);
-      acc[3] = fmaf(raw[i].w, w, acc[3]);
-    }
-    M = bm;
-  }
-#pragma unroll
-  for (int o = 16; o < 64; o <<= 1)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) acc[e] += __shfl_xor(acc[e], o);
-  DKV_TL(tl_comb, 2);
-  if (j != 0) return;
-  const float inv = 1.f / L;
-  const float v0 = acc[0] * inv, v1 = acc[1] * inv, v2 = acc[2] * inv, v3 = acc[3] * inv;
-  const int gq = r / a.nq, m = r - gq * a.nq;
-  const int64_t off = (int64_t)m * a.out_tok_stride + (int64_t)(h * G + gq) * a.out_head_stride + 4 * c;
-  if (a.out_dtype == 1)
-    *reinterpret_cast<float4*>(static_cast<float*>(a.out) + off) = make_float4(v0, v1, v2, v3);
-  else
-    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + off) =
-        make_uint2(f32_to_bf16_rne(v0) | (f32_to_bf16_rne(v1) << 16), f32_to_bf16_rne(v2) | (f32_to_bf16_rne(v3) << 16));
+  merge_row_f32(a, h, r, R, G, splits, active, part_o, part_ml);
   DKV_TL(tl_comb, 3);
 }
 
-// Precision-0 merge (fp16 O / sum partials, 128 bytes per row in half_slot()
-// order): one wave per query row. Lane l = 8 j + c reads 16-byte chunk c of
-// split s0 + 8 i + j for i = 0..7, so each load instruction covers 8 splits,
-// and accumulates 8 columns weighted by that split's sum * 2^(m_s - M)
-// (fetched from lane s with a shuffle). The 8 lanes of one chunk are summed
-// at the end, and lanes 0..7 store the row.
 __global__ void __launch_bounds__(256)
 combine_half_kernel(dkv_attn_args a, int splits, int cap, int short_plan, const float* __restrict__ part_o,
                     const float2* __restrict__ part_ml) {
@@ -334,7 +273,6 @@ combine_half_kernel(dkv_attn_args a, int splits, int cap, int short_plan, const 
   const int G = a.q_heads / a.heads;
   const int R = G * a.nq;
   const int r = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
   if (r >= R) return;
   int units = a.n_tiles + (a.nq + TILE - 1) / TILE;
   Hist hs;
@@ -342,71 +280,7 @@ combine_half_kernel(dkv_attn_args a, int splits, int cap, int short_plan, const 
   const int active = short_plan ? short_runtime_plan(a, hs, units, splits) : runtime_plan(a, hs, units, splits, cap);
   if (active <= 1) return;  // one split ran and stored the output itself
   DKV_TL(tl_comb, 1);
-  const int64_t base = (int64_t)h * splits * R + r;
-  const int j = lane >> 3, c = lane & 7;
-  const uint4* rows = reinterpret_cast<const uint4*>(part_o);  // 8 chunks of 16 bytes per row
-  float M = -INFINITY, L = 0.f, acc[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-  for (int s0 = 0; s0 < active; s0 += 64) {
-    const int cnt = min(64, active - s0);
-    const float2 ml = lane < cnt ? part_ml[base + (int64_t)(s0 + lane) * R] : make_float2(-INFINITY, 0.f);
-    uint4 raw[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int s = 8 * i + j;
-      const u32x4* src = reinterpret_cast<const u32x4*>(rows) + (base + (int64_t)(s0 + s) * R) * 8 + c;
-      raw[i] = s < cnt ? __builtin_bit_cast(uint4, __builtin_nontemporal_load(src)) : make_uint4(0, 0, 0, 0);
-    }
-    float bm = ml.x;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) bm = fmaxf(bm, __shfl_xor(bm, o));
-    bm = fmaxf(bm, M);
-    if (bm == -INFINITY) continue;  // wave-uniform: every split so far saw no visible key
-    const float f = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - bm);
-    int ex;
-    float lsum = half_partial_decode(ml.y, ex) * f;
-    const float wsplit = ex ? __builtin_amdgcn_ldexpf(lsum, ex) : lsum;  // weight of the stored O / sum / 2^ex
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o);
-    const float f0 = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - bm);
-    L = fmaf(L, f0, lsum);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] *= f0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float w = __shfl(wsplit, 8 * i + j);  // 0 for splits past cnt
-      const uint32_t q[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const _Float16 lo = __builtin_bit_cast(_Float16, (uint16_t)(q[e] & 0xffffu));
-        const _Float16 hi = __builtin_bit_cast(_Float16, (uint16_t)(q[e] >> 16));
-        acc[2 * e] = fmaf((float)lo, w, acc[2 * e]);
-        acc[2 * e + 1] = fmaf((float)hi, w, acc[2 * e + 1]);
-      }
-    }
-    M = bm;
-  }
-#pragma unroll
-  for (int o = 8; o < 64; o <<= 1)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], o);
-  DKV_TL(tl_comb, 2);
-  if (j != 0) return;
-  const float inv = 1.f / L;
-  const int gq = r / a.nq, m = r - gq * a.nq;
-  const int64_t off = (int64_t)m * a.out_tok_stride + (int64_t)(h * G + gq) * a.out_head_stride;
-#pragma unroll
-  for (int half = 0; half < 2; ++half) {  // slots 8c + 4 half + [0, 4): 4 consecutive columns
-    const int col = half_column(8 * c + 4 * half);
-    const float v0 = acc[4 * half] * inv, v1 = acc[4 * half + 1] * inv;
-    const float v2 = acc[4 * half + 2] * inv, v3 = acc[4 * half + 3] * inv;
-    if (a.out_dtype == 1)
-      *reinterpret_cast<float4*>(static_cast<float*>(a.out) + off + col) = make_float4(v0, v1, v2, v3);
-    else
-      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + off + col) =
-          make_uint2(f32_to_bf16_rne(v0) | (f32_to_bf16_rne(v1) << 16), f32_to_bf16_rne(v2) | (f32_to_bf16_rne(v3) << 16));
-  }
+  merge_row_half(a, h, r, R, G, splits, active, part_o, part_ml);
   DKV_TL(tl_comb, 3);
 }
 
@@ -522,8 +396,8 @@ static Plan make_plan(const dkv_attn_args& a) {
     const int per = a.heads * p.row_groups;
     if (p.path == 3) {
       // two waves per unit, four units per workgroup: every tile of the history is requested
-      // when the kernel starts
-      splits = (p.units + SHORT_UNITS - 1) / SHORT_UNITS;
+      // when the kernel starts (at most SHORT_MAX_SPLITS workgroups per KV head)
+      splits = short_default_splits(p.units);
     } else {
       // MFMA: one 12-wave workgroup per CU, all resident at once (a grid one past the CU count
       // would take a second round for a single workgroup); balanced over the history. A launch
@@ -537,6 +411,8 @@ static Plan make_plan(const dkv_attn_args& a) {
   if (splits > p.units) splits = p.units;
   if (splits < 1) splits = 1;
   p.splits = splits;
+  p.fused = DKV_INKERNEL_MERGE && a.path == 0 && p.path == 2 && p.precision == 0 && splits > 1 &&
+            a.heads * p.row_groups * 4 <= INKERNEL_COUNTER_BYTES;
   if (splits > 1) {
     if (p.path == 3) {  // unnormalized fp32 O and (max, sum), as combine_kernel reads them
       p.part_o_bytes = (int64_t)a.heads * splits * R * D * 4;
@@ -551,6 +427,12 @@ static Plan make_plan(const dkv_attn_args& a) {
   return p;
 }
 
+// Workspace bytes of a plan: the split partials (none for one split), after the arrival counters in
+// the in-kernel merge build.
+static int64_t workspace_bytes(const Plan& p) {
+  return p.splits > 1 ? INKERNEL_COUNTER_BYTES + p.part_o_bytes + p.part_ml_bytes : 0;
+}
+
 int launch_attn_vec(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml, hipStream_t s) {
   const dim3 grid(p.splits, a.heads, p.row_groups);
   if (p.precision == 1)
@@ -563,15 +445,16 @@ int launch_attn_vec(const dkv_attn_args& a, const Plan& p, float* part_o, float2
 }
 
 // The launches of one attention call whose split partials go to `ws` (at least
-// p.part_o_bytes + p.part_ml_bytes bytes, or unused for one split).
+// workspace_bytes(p) bytes, or unused for one split).
 static int launch_attend(const dkv_attn_args& a, const Plan& p, void* ws, hipStream_t s) {
-  float* part_o = static_cast<float*>(ws);
-  float2* part_ml = reinterpret_cast<float2*>(static_cast<char*>(ws) + p.part_o_bytes);
+  uint32_t* counters = static_cast<uint32_t*>(ws);
+  float* part_o = reinterpret_cast<float*>(static_cast<char*>(ws) + INKERNEL_COUNTER_BYTES);
+  float2* part_ml = reinterpret_cast<float2*>(static_cast<char*>(ws) + INKERNEL_COUNTER_BYTES + p.part_o_bytes);
   const int rc = p.path == 3 ? launch_attn_short(a, p, part_o, part_ml, s)
-                 : p.path == 2 ? launch_attn_mfma(a, p, part_o, part_ml, s)
+                 : p.path == 2 ? launch_attn_mfma(a, p, part_o, part_ml, counters, s)
                                : launch_attn_vec(a, p, part_o, part_ml, s);
   if (rc) return rc;
-  if (p.splits > 1) {
+  if (p.splits > 1 && !p.fused) {
     const int R = (a.q_heads / a.heads) * a.nq;
     const int short_plan = p.path == 3;
     if (p.precision == 1 || short_plan)  // the short-chunk kernel's partials are fp32 in both precisions
@@ -628,8 +511,7 @@ extern "C" {
 int64_t dkv_attend_workspace_bytes(const dkv_attn_args* args) {
   if (!args || args->heads <= 0 || args->q_heads <= 0 || args->q_heads % args->heads || args->nq <= 0)
     return 0;
-  const Plan p = make_plan(*args);
-  return p.part_o_bytes + p.part_ml_bytes;
+  return workspace_bytes(make_plan(*args));
 }
 
 int dkv_attend(const dkv_attn_args* args, void* stream) {
@@ -641,7 +523,7 @@ int dkv_attend(const dkv_attn_args* args, void* stream) {
   const dkv_attn_args& a = *args;
   if (int rc = check_args(a)) return rc;
   const Plan p = make_plan(a);
-  const int64_t need = p.part_o_bytes + p.part_ml_bytes;
+  const int64_t need = workspace_bytes(p);
   if (need > 0 && (!a.workspace || a.workspace_bytes < need)) {
     set_error("dkv_attend: workspace of %lld bytes needed, %lld given", (long long)need,
               (long long)a.workspace_bytes);
@@ -659,7 +541,7 @@ int dkv_attend_noalloc(const dkv_attn_args* args, void* stream) {
   const dkv_attn_args& a = *args;
   if (int rc = check_args(a)) return rc;
   const Plan p = make_plan(a);
-  const int64_t need = p.part_o_bytes + p.part_ml_bytes;
+  const int64_t need = workspace_bytes(p);
   if (need > DKV_NOALLOC_SCRATCH_BYTES) {
     set_error("dkv_attend_noalloc: this call's split partials need %lld bytes, more than the %d-byte "
               "scratch buffer (use dkv_attend with a workspace, or fewer splits)",

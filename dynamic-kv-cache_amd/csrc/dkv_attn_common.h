@@ -15,7 +15,7 @@ constexpr float LOG2E = 1.4426950408889634f;
 // which that build's dkv_timeline_*() export copies out. Used to see where a
 // launch's time goes (which memory round trips sit on the critical path).
 #ifdef DKV_TIMELINE
-constexpr int TL_EVENTS = 8;
+constexpr int TL_EVENTS = 10;  // 8 and 9: the in-kernel merge build's
 constexpr int TL_SLOTS = 1 << 14;  // workgroups recorded per launch
 #define DKV_TL(buf, ev)                                                                        \
   do {                                                                                         \
@@ -145,7 +145,7 @@ __device__ __forceinline__ int runtime_plan(const dkv_attn_args& a, Hist& hs, in
 }
 
 // The same for the short-chunk kernel, whose default split count is
-// ceil(units / SHORT_UNITS) workgroups per KV head rather than the launch's
+// short_default_splits(units) workgroups per KV head rather than the launch's
 // count: the splits that run for the runtime history are the ones a direct
 // call on that history runs (an explicit args.splits keeps its meaning), never
 // more than the launch's grid (nwg). The merge kernel that reads the short
@@ -176,6 +176,17 @@ __device__ __forceinline__ int chunk_seg_start(const dkv_attn_args& a, int j) {
 // [heads, splits, R] float2.
 // The short-chunk kernel writes fp32 partials (precision-1 layout) in both
 // precisions.
+//
+// The in-kernel merge build (-DDKV_INKERNEL_MERGE=1, _build.py --in-kernel-merge;
+// a measurement build, not the library the package loads): the auto path's
+// precision-0 calls skip the merge kernel, and the last workgroup of each (KV
+// head, row group) to store its partials merges all of them. Its workspaces
+// start with INKERNEL_COUNTER_BYTES of arrival counters, zero before first use
+// and left zero by every call.
+#ifndef DKV_INKERNEL_MERGE
+#define DKV_INKERNEL_MERGE 0
+#endif
+constexpr int INKERNEL_COUNTER_BYTES = DKV_INKERNEL_MERGE ? 4096 : 0;
 struct Plan {
   int path;       // 1 vector, 2 MFMA, 3 short chunk
   int precision;  // 0 bf16 operands (reference rounding), 1 fp32-accurate
@@ -184,18 +195,28 @@ struct Plan {
   int row_groups;
   int rows_per_group;
   int cap;        // default split cap (0: the caller's explicit split count)
+  int fused;      // the in-kernel merge build: the frame-chunk kernel merges its own splits
   int64_t part_o_bytes, part_ml_bytes;
 };
 
 // Launchers (return hipGetLastError()).
 int launch_attn_vec(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml,
                     hipStream_t s);
-int launch_attn_mfma(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml,
+int launch_attn_mfma(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml, uint32_t* counters,
                      hipStream_t s);
 int launch_attn_short(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml, hipStream_t s);
 
 constexpr int SHORT_ROWS = 16;  // query rows per KV head the short-chunk kernel takes (one MFMA block)
 constexpr int SHORT_UNITS = 4;  // 64-key units per short-chunk workgroup (one per wave) by default
+// Most short-chunk workgroups per KV head by default: histories past 4 * 64 units (16k tokens) give
+// each workgroup more than SHORT_UNITS units instead of growing the grid. It also bounds the grid of a
+// launch sized for a device step pair, whose bound is the cache's whole tile table.
+constexpr int SHORT_MAX_SPLITS = 64;
+// Default split count of the short-chunk kernel over `units` units.
+__host__ __device__ inline int short_default_splits(int units) {
+  const int s = (units + SHORT_UNITS - 1) / SHORT_UNITS;
+  return s < 1 ? 1 : (s > SHORT_MAX_SPLITS ? SHORT_MAX_SPLITS : s);
+}
 constexpr int VEC_ROWS = 64;    // query rows per vector-path workgroup
 
 __device__ __forceinline__ int short_runtime_plan(const dkv_attn_args& a, Hist& hs, int& units, int nwg) {
@@ -206,7 +227,7 @@ __device__ __forceinline__ int short_runtime_plan(const dkv_attn_args& a, Hist& 
     hs.n_tiles = a.step[1];
     units = hs.n_tiles + (a.nq + TILE - 1) / TILE;
   }
-  const int want = a.splits > 0 ? min(a.splits, units) : (units + SHORT_UNITS - 1) / SHORT_UNITS;
+  const int want = a.splits > 0 ? min(a.splits, units) : short_default_splits(units);
   return max(1, min(nwg, want));
 }
 constexpr int MFMA_ROWS = 192;  // query rows per MFMA-path workgroup (6 waves x 2 blocks x 16)

@@ -36,10 +36,20 @@
 // PREC 0 (combine_half_kernel; rows past the fp16 range are stored scaled,
 // see half_partial_exponent). The partials are stored nontemporally: the end
 // of a kernel writes every dirty L2 line back, and partials kept out of L2
-// leave nothing to write back (3 us less per launch at past 8128). (Merging
-// in the last-arriving workgroup instead needs a device-scope fence per
-// workgroup, which on gfx950 writes back and invalidates the XCD's L2 and
-// cost far more than the second launch.)
+// leave nothing to write back (3 us less per launch at past 8128).
+//
+// The in-kernel merge build (DKV_INKERNEL_MERGE, a measurement build) merges
+// the splits in this launch instead: each workgroup waits for its precision-0
+// partial stores (vmcnt 0) and counts its arrival on its (KV head, row
+// group)'s counter with an agent-scope release; the workgroup that arrives
+// last acquires, resets the counter for the next launch and merges every split
+// with the merge kernel's row arithmetic (dkv_merge.h), so the output bits
+// equal the two-launch path's. No workgroup waits for another. Timed on this
+// kernel, the arrival comes 2-3 us after a workgroup's stores, and one
+// workgroup then reads all of its KV head's partials: decode steps at past
+// 8128 ran 13.8 us against 11.7 with the second launch, and a 64-token frame
+// chunk (192 rows x 43 splits, 1.1 MB of partials per KV head) 55.6 us
+// against 16.1, so the library keeps the merge kernel.
 //
 // Precision (template PREC):
 //   0  the reference kernel's rounding points (src/gpu_kernels.py:93-102):
@@ -49,6 +59,7 @@
 //      O = P_hi V_hi + P_hi V_lo + P_lo V_hi; the lo terms are skipped for
 //      bf16 units, where they are exactly zero.
 #include "dkv_attn_common.h"
+#include "dkv_merge.h"
 #include <type_traits>
 
 namespace dkv {
@@ -195,7 +206,8 @@ __device__ __forceinline__ Unit unit_at(const dkv_attn_args& a, const Hist& hs, 
 // store only real rows.
 #ifdef DKV_TIMELINE
 // events: 0 entry, 1 first unit staged in LDS, 2 first unit dequantized, 3 first unit computed,
-// 4 last unit computed, 5 key groups merged, 6 stores issued, 7 arguments arrived
+// 4 last unit computed, 5 key groups merged, 6 stores issued, 7 arguments arrived; in the in-kernel
+// merge build also 8 arrival counted, 9 splits merged and stored (by the last workgroup only)
 static __device__ uint64_t tl_mfma[TL_SLOTS * TL_EVENTS];
 #endif
 
@@ -204,7 +216,11 @@ static __device__ uint64_t tl_mfma[TL_SLOTS * TL_EVENTS];
 template <int PREC, int NBW, bool ARGT>
 __global__ void __launch_bounds__(MF_THREADS)
 attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dkv_attn_args a, int units,
-                 int splits, int cap, int rpg, float* __restrict__ part_o, float2* __restrict__ part_ml) {
+                 int splits, int cap, int rpg, float* __restrict__ part_o, float2* __restrict__ part_ml
+#if DKV_INKERNEL_MERGE
+                 , int fused, uint32_t* __restrict__ counters
+#endif
+                 ) {
   // LDS: two raw stages of (K, V) sub-blocks and two sets of bf16 tiles
   // (K, V^T, and for PREC 1 their lo parts). After the last unit the same
   // bytes hold the key-group merge (O rows, then (max, sum) pairs).
@@ -618,10 +634,43 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
     }
   }
   DKV_TL(tl_mfma, 6);
+#if DKV_INKERNEL_MERGE
+  if constexpr (PREC == 0) {
+    if (!fused || active <= 1) return;
+    __shared__ int merge_here;
+    __builtin_amdgcn_s_waitcnt(0);  // every wave's partial stores have completed
+    __syncthreads();
+    if (t == 0) {  // the release writes the XCD's L2 back, so all of the workgroup's partials
+      uint32_t* ctr = counters + h * gridDim.z + rg;
+      const uint32_t ticket = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+      merge_here = ticket == (uint32_t)(active - 1);
+      if (merge_here) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next launch
+    }
+    __syncthreads();
+    DKV_TL(tl_mfma, 8);
+    if (!merge_here) return;
+    if (wave == 0) {  // acquire for the workgroup: invalidate the CU's L1 and the XCD's L2, and wait
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      __builtin_amdgcn_s_waitcnt(0);
+    }
+    __syncthreads();
+#pragma unroll 1
+    for (int r = r0 + wave; r < r_end; r += MF_THREADS / 64)
+      merge_row_half(a, h, r, R, G, splits, active, part_o, part_ml);
+    DKV_TL(tl_mfma, 9);
+  }
+#endif
 }
 
+#if DKV_INKERNEL_MERGE
+#define DKV_MERGE_ARGS , p.fused, counters
+#else
+#define DKV_MERGE_ARGS
+#endif
+
 template <int PREC>
-static void launch_prec(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml, hipStream_t s) {
+static void launch_prec(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml, uint32_t* counters,
+                        hipStream_t s) {
   const dim3 grid(p.splits, a.heads, p.row_groups);
   const int nbw = (p.rows_per_group / 16 + KG_WAVES - 1) / KG_WAVES;  // blocks of the busiest wave (<= 2)
   ArgTiles at;
@@ -630,22 +679,23 @@ static void launch_prec(const dkv_attn_args& a, const Plan& p, float* part_o, fl
   if (fill_arg_tiles(a, at)) {
     if (nbw >= 2)
       hipLaunchKernelGGL((attn_mfma_kernel<PREC, 2, true>), grid, dim3(MF_THREADS), 0, s, at, a, p.units, p.splits,
-                         p.cap, rpg, part_o, part_ml);
+                         p.cap, rpg, part_o, part_ml DKV_MERGE_ARGS);
     else
       hipLaunchKernelGGL((attn_mfma_kernel<PREC, 1, true>), grid, dim3(MF_THREADS), 0, s, at, a, p.units, p.splits,
-                         p.cap, rpg, part_o, part_ml);
+                         p.cap, rpg, part_o, part_ml DKV_MERGE_ARGS);
   } else if (nbw >= 2) {
     hipLaunchKernelGGL((attn_mfma_kernel<PREC, 2, false>), grid, dim3(MF_THREADS), 0, s, none, a, p.units, p.splits,
-                       p.cap, rpg, part_o, part_ml);
+                       p.cap, rpg, part_o, part_ml DKV_MERGE_ARGS);
   } else {
     hipLaunchKernelGGL((attn_mfma_kernel<PREC, 1, false>), grid, dim3(MF_THREADS), 0, s, none, a, p.units, p.splits,
-                       p.cap, rpg, part_o, part_ml);
+                       p.cap, rpg, part_o, part_ml DKV_MERGE_ARGS);
   }
 }
 
-int launch_attn_mfma(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml, hipStream_t s) {
-  if (p.precision == 1) launch_prec<1>(a, p, part_o, part_ml, s);
-  else launch_prec<0>(a, p, part_o, part_ml, s);
+int launch_attn_mfma(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml, uint32_t* counters,
+                     hipStream_t s) {
+  if (p.precision == 1) launch_prec<1>(a, p, part_o, part_ml, counters, s);
+  else launch_prec<0>(a, p, part_o, part_ml, counters, s);
   return (int)hipGetLastError();
 }
 

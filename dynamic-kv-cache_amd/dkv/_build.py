@@ -25,6 +25,11 @@ LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 # wall-clock stamps that dkv_timeline_short / dkv_timeline_mfma copy out. A diagnostic library,
 # never the one the package loads unless bench.py --timeline points it there.
 TIMELINE_LIB_PATH = os.path.join(PKG_DIR, 'libdkv_timeline.so')
+# The in-kernel merge build (-DDKV_INKERNEL_MERGE=1): the frame-chunk kernel merges its own history
+# splits (the last workgroup of each KV head) instead of a second launch. A measurement build for
+# bench.py --lib, slower than the library's two launches at every shape timed.
+INKERNEL_LIB_PATH = os.path.join(PKG_DIR, 'libdkv_inkernel_merge.so')
+INKERNEL_TIMELINE_LIB_PATH = os.path.join(PKG_DIR, 'libdkv_inkernel_merge_timeline.so')
 ARCH = os.environ.get('DKV_OFFLOAD_ARCH', 'gfx950')
 
 HIPCC_FLAGS = [
@@ -62,7 +67,8 @@ def build(verbose=False, extra=(), out=None):
 
 
 if __name__ == '__main__':
-    if '--timeline' in sys.argv[1:]:
-        print(build(verbose=True, extra=['-DDKV_TIMELINE'], out=TIMELINE_LIB_PATH))
-    else:
-        print(build(verbose=True))
+    timeline, inkernel = '--timeline' in sys.argv[1:], '--in-kernel-merge' in sys.argv[1:]
+    extra = (['-DDKV_TIMELINE'] if timeline else []) + (['-DDKV_INKERNEL_MERGE=1'] if inkernel else [])
+    out = {(False, False): LIB_PATH, (True, False): TIMELINE_LIB_PATH, (False, True): INKERNEL_LIB_PATH,
+           (True, True): INKERNEL_TIMELINE_LIB_PATH}[(timeline, inkernel)]
+    print(build(verbose=True, extra=extra, out=out))

@@ -773,12 +773,19 @@ class GraphSteps:
         # Launch bounds: the largest history a chunk can attend to in this cache.
         self.past_bound = cache.capacity - chunk
         self.tiles_bound = cache.tiles.shape[0]
-        self.ws = None  # attention workspace of the recorded launches (grow-only, before capture)
+        self.ws = None  # attention workspace of the recorded launches (grow-only)
+        self.retired = []  # smaller workspaces handed out before: graphs captured earlier still address them
 
     def workspace(self, nbytes):
+        """The attention workspace graph launches use, at least `nbytes` bytes. A buffer once handed
+        out is never freed while the steps live, even when a later call needs a larger one: a graph
+        captured with it (on these steps, or re-attached ones) keeps writing its partials there."""
         if self.ws is None or self.ws.numel() < nbytes:
+            if self.ws is not None:
+                self.retired.append(self.ws)
+            grow = 2 * self.ws.numel() if self.ws is not None else 0
             with torch.inference_mode(False):
-                self.ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=self.cache.device)
+                self.ws = torch.zeros(max(nbytes, grow, 1 << 20), dtype=torch.uint8, device=self.cache.device)
         return self.ws
 
     def _check_storage(self):

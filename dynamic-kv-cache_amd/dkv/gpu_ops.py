@@ -166,8 +166,12 @@ def _layer_plan(layer, n, width):
     plans = layer.__dict__.setdefault('_dkv_plans', {})
     attn, mlp = layer.self_attn, layer.mlp
     p = plans.get((n, width))
-    if p is not None and p.holds(layer):
-        return p
+    if p is not None:
+        if p.holds(layer):
+            return p
+        # the layer holds other weights now: every plan of it (other chunk lengths too) still refers
+        # to the old tensors, which would stay alive with them
+        plans.clear()
     ln1, ln2 = layer.input_layernorm, layer.post_attention_layernorm
     o_w, d_w = attn.o_proj.weight, mlp.down_proj.weight
     if not (attn.o_proj.bias is None and mlp.down_proj.bias is None

@@ -95,7 +95,8 @@ typedef struct dkv_attn_args {
   int32_t splits;        /* 0 = auto; history split count per KV head */
   int32_t precision;     /* 0 = the reference kernel's bf16 rounding of K, V and p
                             (src/gpu_kernels.py:93-94,102); 1 = fp32-accurate */
-  void* workspace;       /* device scratch of dkv_attend_workspace_bytes() */
+  void* workspace;       /* device scratch of dkv_attend_workspace_bytes() (0 for one split): the
+                            split partials; a workspace serves one call at a time */
   int64_t workspace_bytes;
   const int32_t* step;   /* NULL, or a DEVICE pair {past, n_tiles} read when the kernels run,
                             for launches recorded once in a HIP graph and replayed as the
@@ -107,7 +108,12 @@ typedef struct dkv_attn_args {
                             (read beside the arguments) instead of waiting on the device table
                             before its first history loads; otherwise it is ignored. A copy whose
                             tiles are not well formed or do not cover [0, past) in token order is
-                            refused (DKV_EINVAL). */
+                            refused (DKV_EINVAL). The descriptors are copied into the launch when
+                            dkv_attend is called, so a launch captured in a HIP graph keeps the
+                            ones it was captured with: its replays read the tiles as they were then
+                            (offsets, widths, rows), not the device table. Capture launches that
+                            must follow a table that changes (a cache reset, appends at other
+                            widths) with `step`, or with tiles_host = NULL. */
 } dkv_attn_args;
 
 /* One segment of the arena in the reference's CPU-cache layout: what
@@ -182,9 +188,10 @@ int64_t dkv_attend_workspace_bytes(const dkv_attn_args* args);
 
 /* Fused packed-history causal GQA attention. Replaces GPUCache.attend's
  * packed_attention launch (src/gpu_cache.py:96-104, src/gpu_kernels.py:71-105).
- * Frame chunks run a split-history MFMA kernel, short chunks (at most 16 query
- * rows per KV head, e.g. decode steps) a kernel with one wave per 64-key tile;
- * a merge kernel combines the history splits of either.
+ * Every chunk length runs a split-history MFMA kernel by default (path 0/2);
+ * path 3 runs short chunks (at most 16 query rows per KV head, e.g. decode
+ * steps) on a kernel with two waves per 64-key tile. A merge kernel combines
+ * the history splits of either in a second launch.
  * Output rows are written to out + m*out_tok_stride + qh*out_head_stride
  * (elements), the reference's [1, nq, q_heads, 64] layout when contiguous.
  * Q, K and V must be 16-byte aligned with strides in multiples of 8 elements;

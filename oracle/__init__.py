@@ -10,7 +10,6 @@ Modules:
   attention        dequantize-then-SDPA oracles (fp64/fp32) and the reference
                    GPU kernel's bf16 rounding semantics (src/gpu_kernels.py:71-105)
   cpu_path         the reference CPU cache flow (src/cache_manager.py:17-90)
-  arena            byte-level model of libdkv's arena for one layer/head
 
 Pinning (how each function is checked beyond retyping its formula) is listed in
 each module's docstring and tested in tests/test_oracle_*.py.

@@ -203,8 +203,8 @@ def test_attend_demands_workspace_when_split():
 def test_attend_workspace_matches_the_partial_format():
     """Per split row: 64 fp16 O / sum values + (max, sum) in bf16 precision, 64 fp32 O + (max, sum)
     in fp32 precision; the short-chunk kernel (path 3) keeps fp32 rows in both precisions, one
-    split per 4 units (64-token tiles plus the chunk) by default. Auto takes the frame-chunk
-    kernel for decode steps too."""
+    split per 4 units (64-token tiles plus the chunk) by default, at most 64 per KV head. Auto
+    takes the frame-chunk kernel for decode steps too. One split needs no workspace."""
     lib = _lib.load()
     need = {}
     for precision in (0, 1):
@@ -216,6 +216,10 @@ def test_attend_workspace_matches_the_partial_format():
         a = attn(past=4096, n_tiles=64, arena=4096, tiles=4096, nq=1, precision=precision, path=3)
         splits = (64 + 1 + 3) // 4
         assert lib.dkv_attend_workspace_bytes(ctypes.byref(a)) == a.heads * splits * 3 * (64 * 4 + 8)
+        long = attn(past=64 * 600, n_tiles=600, arena=4096, tiles=4096, nq=1, precision=precision, path=3)
+        assert lib.dkv_attend_workspace_bytes(ctypes.byref(long)) == long.heads * 64 * 3 * (64 * 4 + 8)
+        one = attn(past=4096, n_tiles=64, arena=4096, tiles=4096, nq=1, precision=precision, splits=1)
+        assert lib.dkv_attend_workspace_bytes(ctypes.byref(one)) == 0
         auto = attn(past=4096, n_tiles=64, arena=4096, tiles=4096, nq=1, precision=precision)
         mfma = attn(past=4096, n_tiles=64, arena=4096, tiles=4096, nq=1, precision=precision, path=2)
         assert lib.dkv_attend_workspace_bytes(ctypes.byref(auto)) == lib.dkv_attend_workspace_bytes(ctypes.byref(mfma))

@@ -73,16 +73,18 @@ def run(c, q, kn, vn, past, path, precision, with_table, splits=0):
     return out
 
 
-@pytest.mark.parametrize('past,nq', [(2000, 64), (8128, 64), (8128, 1), (700, 4), (70, 37)])
-@pytest.mark.parametrize('path', ['auto', 'mfma', 'short'])
+SHAPES = [(2000, 64), (8128, 64), (8128, 1), (700, 4), (70, 37)]
+# the short-chunk kernel takes at most 16 query rows per KV head (3 * nq <= 16 with 3-way GQA)
+CASES = [(past, nq, path) for past, nq in SHAPES for path in ('auto', 'mfma', 'short')
+         if path != 'short' or 3 * nq <= 16]
+
+
+@pytest.mark.parametrize('past,nq,path', CASES)
 @pytest.mark.parametrize('precision', ['bf16', 'fp32'])
 def test_descriptors_in_the_argument_block_give_the_same_bits(cuda, past, nq, path, precision):
     """Histories of 2 to 127 tiles (mixed widths, a partial last tile at 2000 and 700), frame
-    chunks and decode steps on the frame-chunk and short-chunk kernels (the latter takes at most
-    16 query rows per KV head), one split and the default plan: the same output bits with the
-    host copy passed as without it."""
-    if path == 'short' and 3 * nq > 16:
-        pytest.skip('the short-chunk kernel takes at most 16 query rows per KV head')
+    chunks and decode steps on the frame-chunk and short-chunk kernels, one split and the default
+    plan: the same output bits with the host copy passed as without it."""
     announce(f'argument-block descriptors past={past} nq={nq} path={path} precision={precision}')
     case = frame_chunk_case(past, seed=past + nq, nq=nq)
     heads = case['k_hist'].shape[0]

@@ -457,10 +457,11 @@ def test_ill_conditioned_rows_dequantize_like_unpack(cuda, nq, paths):
 @pytest.mark.parametrize('precision', ['fp32', 'bf16'])
 @pytest.mark.parametrize('past,nq', [(0, 1), (1, 1), (63, 4), (64, 5), (700, 1), (1000, 3), (8128, 1), (8128, 4)])
 def test_short_chunk_kernel(cuda, past, nq, precision):
-    """The short-chunk kernel (one wave per 64-key unit, splits merged by the last workgroup in the
-    same launch) against the oracles: fp32 precision within 1e-3 of the fp64 oracle, bf16 within
-    max(2e-2, the reference's own p-rounding noise) of the emulated reference; and equal to the
-    frame-chunk MFMA kernel's result on the same call within those bounds."""
+    """The short-chunk kernel (two waves per 64-key unit; the split partials are merged by
+    combine_kernel in a second launch) against the oracles: fp32 precision within 1e-3 of the
+    fp64 oracle, bf16 within max(2e-2, the reference's own p-rounding noise) of the emulated
+    reference; and equal to the frame-chunk MFMA kernel's result on the same call within those
+    bounds."""
     announce(f'attention short path past={past} nq={nq} precision={precision}')
     case = frame_chunk_case(past, seed=300 + past + nq, nq=nq)
     c, dk, dv = build(case, cuda)
@@ -522,14 +523,17 @@ def test_short_chunk_rejects_too_many_rows(cuda):
         c.attend(q, kn, vn, 0, past, path='short')
 
 
+@pytest.mark.parametrize('path', ['auto', 'short'])
 @pytest.mark.parametrize('precision', ['fp32', 'bf16'])
-def test_decode_steps_replayed_from_a_graph(cuda, precision):
+def test_decode_steps_replayed_from_a_graph(cuda, precision, path):
     """One-token decode steps (pack the token, attend over the history before it) recorded once in
     a HIP graph (the launches sized for the cache's capacity, the history read from the device step
     pair) and replayed as the history grows from 0 to 9 tiles: every replay's attention must equal a
     direct call on the same history bit for bit (the direct call passes the tile descriptors by
-    value, the replay reads the device table the replays' packs wrote)."""
-    announce(f'attention decode steps graph replay precision={precision}')
+    value, the replay reads the device table the replays' packs wrote). On the short-chunk kernel
+    the replays run 1, 2 and 3 splits (4 units per workgroup) out of a grid sized for the cache's
+    whole tile table, so the merge kernel's single-split return and its split bound are both hit."""
+    announce(f'attention decode steps graph replay precision={precision} path={path}')
     torch.manual_seed(5)
     heads, q_heads = 5, 15
     c = GPUCache(None, layers=1, heads=heads, max_tokens=640, precision=precision)
@@ -542,12 +546,12 @@ def test_decode_steps_replayed_from_a_graph(cuda, precision):
     side = torch.cuda.Stream()
     with torch.cuda.stream(side):
         c.append(kn, vn, 0)
-        c.attend(q, kn, vn, 0, 0)
+        c.attend(q, kn, vn, 0, 0, path=path)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):  # a decode step: pack the token, then attend over the history before it
         c.append(kn, vn, 0)
-        out = c.attend(q, kn, vn, 0, 0)
+        out = c.attend(q, kn, vn, 0, 0, path=path)
     c.end_graph_steps()
     c.reset()
     bits = [4, 8, 16, 4, 8, 4, 16, 8, 4]
@@ -559,7 +563,7 @@ def test_decode_steps_replayed_from_a_graph(cuda, precision):
         c.end_graph_steps()
         got = out.clone()
         c.seen = [past]  # the direct call on the same history (the step's token not appended)
-        ref = c.attend(q, kn, vn, 0, past)
+        ref = c.attend(q, kn, vn, 0, past, path=path)
         torch.cuda.synchronize()
         assert torch.equal(got, ref), (i, (got.float() - ref.float()).abs().max().item())
         c.seen = [past + 1]

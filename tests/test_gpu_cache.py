@@ -152,3 +152,56 @@ def test_graph_launches_keep_their_workspace(cuda):
     graph.replay()
     torch.cuda.synchronize()
     assert past == 128 and torch.equal(out, ref)
+
+
+def test_graph_captured_first_survives_a_larger_capture_on_the_same_steps(cuda):
+    """Two graphs of 5-token steps captured on one GraphSteps: first on the frame-chunk kernel
+    (auto), then on the short-chunk kernel, whose fp32 partials (15 query rows per KV head, 64
+    workgroups per head for a launch sized by the cache's whole tile table: 1.27 MB) need a larger
+    workspace than begin_graph_steps() reserved (1 MiB). The steps hand the second capture a new
+    buffer but keep the first one, so replaying the first graph afterwards must still equal a
+    direct call on the same history, bit for bit."""
+    announce('cache: first graph survives a second capture that grows the steps workspace')
+    g = torch.Generator().manual_seed(43)
+    heads, q_heads = 5, 15
+    c = GPUCache(None, layers=1, heads=heads, max_tokens=2048)
+    q = torch.randn(1, q_heads, 5, 64, generator=g).to(torch.bfloat16).to(cuda)
+    kn = torch.randn(1, heads, 5, 64, generator=g).to(torch.bfloat16).to(cuda)
+    vn = torch.randn(1, heads, 5, 64, generator=g).to(torch.bfloat16).to(cuda)
+    steps = c.begin_graph_steps(5, q_heads=q_heads)
+    graphs, outs, sizes = [], [], []
+    for path in ('auto', 'short'):
+        c.reset()
+        c.begin_graph_steps(5, steps=steps)
+        c.select(16)
+        c.graph_step()
+        side = torch.cuda.Stream()
+        with torch.cuda.stream(side):
+            c.append(kn, vn, 0)
+            c.attend(q, kn, vn, 0, 0, path=path)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            c.append(kn, vn, 0)
+            outs.append(c.attend(q, kn, vn, 0, 0, path=path))
+        graphs.append(graph)
+        sizes.append(steps.ws.numel())
+        c.end_graph_steps()
+    assert sizes[1] > sizes[0] and steps.retired  # the second capture did need more
+    c.reset()
+    for bits in (4, 8, 16, 4, 8, 4, 16, 8, 4, 8):  # 10 tiles: several splits either way
+        c.select(bits)
+        c.append(torch.randn(1, heads, 64, 64, generator=g).to(torch.bfloat16).to(cuda),
+                 torch.randn(1, heads, 64, 64, generator=g).to(torch.bfloat16).to(cuda), 0)
+    past = c.seen[0]
+    for path, graph, out in zip(('auto', 'short'), graphs, outs):
+        f = c.fork()  # same arena and tile table: the steps re-attach to it
+        f.begin_graph_steps(5, steps=steps)
+        f.select(16)
+        f.graph_step()
+        graph.replay()
+        f.end_graph_steps()
+        got = out.clone()
+        ref = c.fork().attend(q, kn, vn, 0, past, path=path)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), (path, (got.float() - ref.float()).abs().max().item())

@@ -173,6 +173,9 @@ def test_eager_fused_layers_follow_weight_changes(cuda):
         layer.self_attn.o_proj.weight = torch.nn.Parameter(layer.self_attn.o_proj.weight.detach() * 0.5,
                                                            requires_grad=False)
     fused, upstream = logits(True), logits(False)
+    # plans of the other chunk lengths (the prefix's, the frames') held the old tensors: dropped
+    plans = layer.__dict__.get('_dkv_plans', {})
+    assert plans and all(p is None or p.holds(layer) for p in plans.values())
     changed = (fused - before).abs().max().item()
     diff = (fused - upstream).abs().max().item()
     print(f'[fused-weights] change {changed:.3e}, fused vs upstream {diff:.3e}', flush=True)

@@ -294,20 +294,19 @@ def test_sdpa_backend_decoder_matches_native_and_fused(cuda):
     assert torch.isfinite(got).all() and err <= 0.3, err
 
 
-FULL_FRAMES = 16
-
-
-def test_full_size_decoder_configuration(cuda):
+@pytest.mark.parametrize('n_frames', [16, 64, 96])
+def test_full_size_decoder_configuration(cuda, n_frames):
     """The metric's end-to-end decoder at its configured size (build_decoder() defaults: 32 layers,
-    hidden 960, 15 / 5 heads, SwiGLU 2560, vocab 49280) over 16 mixed-width frames
-    (src/streaming.py:168-237):
+    hidden 960, 15 / 5 heads, SwiGLU 2560, vocab 49280) over 16, 64 and 96 mixed-width frames, the
+    frame counts bench.py times (src/streaming.py:168-237; 96 frames reach 6,184 cache tokens, 97
+    tiles, and the pipelined replays run 12 history splits):
       - pipelined graph replays (8 frames per group) ingest the cache bit for bit like eager
         launches (arena bytes, bookkeeping, question logits);
       - an all-16-bit packed cache at precision='fp32' gives question logits within 0.25 of native
         DynamicCache + SDPA (32 layers of bf16 GEMMs and bf16 SDPA against the fp32-accurate packed
         kernel; the 2-layer decoder holds 0.05);
       - batched candidate scores equal one fork per candidate within 2e-2."""
-    announce('streaming: full-size decoder, 16 frames')
+    announce(f'streaming: full-size decoder, {n_frames} frames')
     from dkv.workloads import bit_schedule, candidate_lengths
     model = build_decoder(seed=0)
     vocab = model.config.vocab_size
@@ -315,8 +314,8 @@ def test_full_size_decoder_configuration(cuda):
     prefix = torch.randint(0, vocab, (1, 16), generator=g)
     question = torch.randint(0, vocab, (1, 24), generator=g)
     cands = [torch.randint(0, vocab, (1, n), generator=g) for n in candidate_lengths(0, 4)]
-    frames = frames_for(model, FULL_FRAMES, seed=62)
-    bits = bit_schedule(FULL_FRAMES, FULL_FRAMES)
+    frames = frames_for(model, n_frames, seed=62)
+    bits = bit_schedule(n_frames, n_frames)
     assert set(bits) == {4, 8, 16}
 
     dec = StreamingDecoder(model, pipeline=8)
@@ -342,16 +341,16 @@ def test_full_size_decoder_configuration(cuda):
     seq = dec.answer(graph_cache, question, cands)
     bat = dec.answer_batched(graph_cache, question, cands)
     torch.cuda.synchronize()
-    print(f'[full-size] batched vs per-fork candidate scores: {seq.tolist()} / {bat.tolist()}', flush=True)
+    print(f'[full-size {n_frames}] batched vs per-fork candidate scores: {seq.tolist()} / {bat.tolist()}', flush=True)
     assert (seq - bat).abs().max().item() <= 2e-2, (seq, bat)
     dec.graphs = False
 
     ref = native_logits(model, prefix, frames, question)
     exact = StreamingDecoder(model, precision='fp32')
-    cache16 = exact.ingest(prefix, frames, [16] * FULL_FRAMES)
+    cache16 = exact.ingest(prefix, frames, [16] * n_frames)
     got = exact.forward(cache16, ids=question, logits=question.shape[1])
     torch.cuda.synchronize()
     err = (got - ref).abs().max().item()
-    print(f'[full-size] 16-bit packed (fp32) vs native logits: max-abs {err:.4e}, '
+    print(f'[full-size {n_frames}] 16-bit packed (fp32) vs native logits: max-abs {err:.4e}, '
           f'logit scale {ref.abs().max().item():.3f}', flush=True)
     assert err <= 0.25, err
