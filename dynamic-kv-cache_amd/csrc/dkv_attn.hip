@@ -237,7 +237,8 @@ attn_vec_kernel(dkv_attn_args a, int units, int splits, int cap, float* __restri
 }
 
 // Both merges read the partials once, with nontemporal loads (past 8128: 18.7 -> 18.5 us per
-// layer; candidate batches 15.9 -> 15.7 us).
+// layer; candidate batches 15.9 -> 15.7 us), or with plain loads where the producing launch stored
+// them plainly (Plan::plain_parts).
 //
 #ifdef DKV_TIMELINE
 // events (both merge kernels): 0 entry, 1 arguments arrived, 3 row stored
@@ -246,6 +247,7 @@ static __device__ uint64_t tl_comb[TL_SLOTS * TL_EVENTS];
 //
 // The two merge kernels: one wave per query row of a KV head, the row's arithmetic in
 // merge_row_f32 (precision 1) and merge_row_half (precision 0), dkv_merge.h.
+template <bool PLAIN>
 __global__ void __launch_bounds__(256)
 combine_kernel(dkv_attn_args a, int splits, int cap, int short_plan, const float* __restrict__ part_o,
                const float2* __restrict__ part_ml) {
@@ -261,10 +263,11 @@ combine_kernel(dkv_attn_args a, int splits, int cap, int short_plan, const float
   const int active = short_plan ? short_runtime_plan(a, hs, units, splits) : runtime_plan(a, hs, units, splits, cap);
   if (active <= 1) return;  // one split ran and stored the output itself
   DKV_TL(tl_comb, 1);
-  merge_row_f32(a, h, r, R, G, splits, active, part_o, part_ml);
+  merge_row_f32<PLAIN>(a, h, r, R, G, splits, active, part_o, part_ml);
   DKV_TL(tl_comb, 3);
 }
 
+template <bool PLAIN>
 __global__ void __launch_bounds__(256)
 combine_half_kernel(dkv_attn_args a, int splits, int cap, int short_plan, const float* __restrict__ part_o,
                     const float2* __restrict__ part_ml) {
@@ -280,7 +283,7 @@ combine_half_kernel(dkv_attn_args a, int splits, int cap, int short_plan, const 
   const int active = short_plan ? short_runtime_plan(a, hs, units, splits) : runtime_plan(a, hs, units, splits, cap);
   if (active <= 1) return;  // one split ran and stored the output itself
   DKV_TL(tl_comb, 1);
-  merge_row_half(a, h, r, R, G, splits, active, part_o, part_ml);
+  merge_row_half<PLAIN>(a, h, r, R, G, splits, active, part_o, part_ml);
   DKV_TL(tl_comb, 3);
 }
 
@@ -411,6 +414,7 @@ static Plan make_plan(const dkv_attn_args& a) {
   if (splits > p.units) splits = p.units;
   if (splits < 1) splits = 1;
   p.splits = splits;
+  p.plain_parts = p.path == 2 && splits > 1 && mfma_blocks_per_wave(p.rows_per_group) == 1;
   p.fused = DKV_INKERNEL_MERGE && a.path == 0 && p.path == 2 && p.precision == 0 && splits > 1 &&
             a.heads * p.row_groups * 4 <= INKERNEL_COUNTER_BYTES;
   if (splits > 1) {
@@ -457,12 +461,19 @@ static int launch_attend(const dkv_attn_args& a, const Plan& p, void* ws, hipStr
   if (p.splits > 1 && !p.fused) {
     const int R = (a.q_heads / a.heads) * a.nq;
     const int short_plan = p.path == 3;
-    if (p.precision == 1 || short_plan)  // the short-chunk kernel's partials are fp32 in both precisions
-      hipLaunchKernelGGL(combine_kernel, dim3((R + 3) / 4, a.heads), dim3(256), 0, s, a, p.splits, p.cap,
-                         short_plan, part_o, part_ml);
-    else
-      hipLaunchKernelGGL(combine_half_kernel, dim3((R + 3) / 4, a.heads), dim3(256), 0, s, a, p.splits, p.cap,
-                         short_plan, part_o, part_ml);
+    const dim3 grid((R + 3) / 4, a.heads);
+    if (p.precision == 1 || short_plan) {  // the short-chunk kernel's partials are fp32 in both precisions
+      if (p.plain_parts)
+        hipLaunchKernelGGL(combine_kernel<true>, grid, dim3(256), 0, s, a, p.splits, p.cap, short_plan, part_o, part_ml);
+      else
+        hipLaunchKernelGGL(combine_kernel<false>, grid, dim3(256), 0, s, a, p.splits, p.cap, short_plan, part_o, part_ml);
+    } else if (p.plain_parts) {
+      hipLaunchKernelGGL(combine_half_kernel<true>, grid, dim3(256), 0, s, a, p.splits, p.cap, short_plan, part_o,
+                         part_ml);
+    } else {
+      hipLaunchKernelGGL(combine_half_kernel<false>, grid, dim3(256), 0, s, a, p.splits, p.cap, short_plan, part_o,
+                         part_ml);
+    }
   }
   return (int)hipGetLastError();
 }

@@ -196,6 +196,7 @@ struct Plan {
   int rows_per_group;
   int cap;        // default split cap (0: the caller's explicit split count)
   int fused;      // the in-kernel merge build: the frame-chunk kernel merges its own splits
+  int plain_parts;  // MFMA split partials of the one-block-per-wave variant: plain stores and loads
   int64_t part_o_bytes, part_ml_bytes;
 };
 
@@ -206,6 +207,11 @@ int launch_attn_mfma(const dkv_attn_args& a, const Plan& p, float* part_o, float
                      hipStream_t s);
 int launch_attn_short(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml, hipStream_t s);
 
+// The MFMA kernel's workgroup: two key groups of MFMA_KG_WAVES waves; a wave owns the 16-row query
+// blocks w and w + MFMA_KG_WAVES of its group, so a group of rows_per_group rows gives its busiest
+// wave this many blocks (1 or 2; the kernel's NBW variant).
+constexpr int MFMA_KG_WAVES = 6;
+inline int mfma_blocks_per_wave(int rows_per_group) { return (rows_per_group / 16 + MFMA_KG_WAVES - 1) / MFMA_KG_WAVES; }
 constexpr int SHORT_ROWS = 16;  // query rows per KV head the short-chunk kernel takes (one MFMA block)
 constexpr int SHORT_UNITS = 4;  // 64-key units per short-chunk workgroup (one per wave) by default
 // Most short-chunk workgroups per KV head by default: histories past 4 * 64 units (16k tokens) give

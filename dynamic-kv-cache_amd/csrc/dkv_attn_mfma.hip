@@ -34,9 +34,11 @@
 // writes partials to the workspace, (running max, sum) per row plus O: fp32
 // and unnormalized at PREC 1 (combine_kernel merges them), fp16 O / sum at
 // PREC 0 (combine_half_kernel; rows past the fp16 range are stored scaled,
-// see half_partial_exponent). The partials are stored nontemporally: the end
-// of a kernel writes every dirty L2 line back, and partials kept out of L2
-// leave nothing to write back (3 us less per launch at past 8128).
+// see half_partial_exponent). Frame chunks store the partials nontemporally:
+// the end of a kernel writes every dirty L2 line back, and partials kept out
+// of L2 leave nothing to write back (3 us less per launch at past 8128).
+// Launches of one query block per wave (decode steps, short chunks) have
+// small partials and store them plainly (part_store).
 //
 // The in-kernel merge build (DKV_INKERNEL_MERGE, a measurement build) merges
 // the splits in this launch instead: each workgroup waits for its precision-0
@@ -71,7 +73,7 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int KG_WAVES = 6;                // waves per key group
+constexpr int KG_WAVES = MFMA_KG_WAVES;    // waves per key group
 constexpr int MF_THREADS = 2 * KG_WAVES * 64;  // 768
 constexpr int MF_LOADERS = 512;            // threads that load, stage and dequantize a unit
 constexpr int KS = 72;       // LDS row stride, in bf16 elements, of the K and V^T tiles
@@ -115,6 +117,20 @@ __device__ __forceinline__ float group_sum(float x) {
 // so it only skips the rescale when no column's max grew at all.
 template <int PREC>
 constexpr float rescale_log2() { return PREC ? 8.f : 0.f; }
+
+// Split partials: plain stores in the one-block-per-wave variant (NBW 1, at most 96 query rows
+// per group: decode steps and short chunks, whose partials are small, so the end of the kernel
+// writes them back from L2 quickly and the merge finds them in the cache hierarchy); nontemporal
+// stores otherwise, which keep the larger partials of frame chunks from being written back from
+// L2 at the end of the kernel (+3 us at past 8128). A compile-time choice: a runtime branch
+// between the two stores is merged by the compiler into one store without the nontemporal hint.
+template <bool PLAIN, typename T>
+__device__ __forceinline__ void part_store(const T& v, T* p) {
+  if constexpr (PLAIN)
+    *p = v;
+  else
+    __builtin_nontemporal_store(v, p);
+}
 
 // Raw sub-blocks sit in LDS with 16 bytes of padding after every 128 bytes,
 // which spreads the rows a dequantizing wave reads over all banks.
@@ -599,15 +615,15 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
         if (PREC) {
 #pragma unroll
           for (int db = 0; db < 4; ++db)
-            __builtin_nontemporal_store(o[db], reinterpret_cast<f32x4*>(part_o + base * D + 16 * db + 4 * g));
+            part_store<NBW == 1>(o[db], reinterpret_cast<f32x4*>(part_o + base * D + 16 * db + 4 * g));
         } else {  // O / l in fp16, row order of half_slot(): chunks g and 4 + g of the row
           const float inv = l > 0.f ? 1.f / l : 0.f;
           _Float16* ph = reinterpret_cast<_Float16*>(part_o) + base * D + 8 * g;
           const f32x4 a0 = o[0] * inv, a1 = o[1] * inv, a2 = o[2] * inv, a3 = o[3] * inv;
           auto store_row = [&](const f32x4& b0, const f32x4& b1, const f32x4& b2, const f32x4& b3) {
-            __builtin_nontemporal_store(__builtin_convertvector(
+            part_store<NBW == 1>(__builtin_convertvector(
                 (f32x8{b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]}), f16x8), reinterpret_cast<f16x8*>(ph));
-            __builtin_nontemporal_store(__builtin_convertvector(
+            part_store<NBW == 1>(__builtin_convertvector(
                 (f32x8{b2[0], b2[1], b2[2], b2[3], b3[0], b3[1], b3[2], b3[3]}), f16x8),
                 reinterpret_cast<f16x8*>(ph + 32));
           };
@@ -629,7 +645,7 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
             }
           }
         }
-        if (g == 0) __builtin_nontemporal_store((f32x2{mm, l}), reinterpret_cast<f32x2*>(part_ml + base));
+        if (g == 0) part_store<NBW == 1>((f32x2{mm, l}), reinterpret_cast<f32x2*>(part_ml + base));
       }
     }
   }
@@ -656,7 +672,7 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
     __syncthreads();
 #pragma unroll 1
     for (int r = r0 + wave; r < r_end; r += MF_THREADS / 64)
-      merge_row_half(a, h, r, R, G, splits, active, part_o, part_ml);
+      merge_row_half<NBW == 1>(a, h, r, R, G, splits, active, part_o, part_ml);
     DKV_TL(tl_mfma, 9);
   }
 #endif
@@ -672,7 +688,7 @@ template <int PREC>
 static void launch_prec(const dkv_attn_args& a, const Plan& p, float* part_o, float2* part_ml, uint32_t* counters,
                         hipStream_t s) {
   const dim3 grid(p.splits, a.heads, p.row_groups);
-  const int nbw = (p.rows_per_group / 16 + KG_WAVES - 1) / KG_WAVES;  // blocks of the busiest wave (<= 2)
+  const int nbw = mfma_blocks_per_wave(p.rows_per_group);
   ArgTiles at;
   const NoArgTiles none = {0};
   const int rpg = p.rows_per_group;

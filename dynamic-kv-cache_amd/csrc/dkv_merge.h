@@ -1,61 +1,109 @@
 // Split merges of the attention kernels: the arithmetic of one query row, run by one wave. The
 // merge kernels (a second launch) and the frame-chunk kernel's in-kernel merge (the last workgroup
 // of a KV head to finish) both call these, so either path stores the same bits.
+//
+// A wave's lanes are (j, c): c picks a 16-byte chunk of the row, j a residue of the split index.
+// Each lane loads the (max, sum) pair of every split it reads beside that split's O chunk, so the
+// loads form one round trip and each lane computes its own splits' weights. The only exchanges
+// are reductions over j, done on the VALU (DPP row_ror and the gfx950 permlane swaps) rather than
+// through LDS: a chain of dependent ds_bpermute shuffles made most of the merge's latency.
 #pragma once
 #include "dkv_attn_common.h"
 
 namespace dkv {
 
+typedef float merge_f32x2 __attribute__((ext_vector_type(2)));
+
+// Partials of launches with few query rows (one 16-row block per wave) are written with plain
+// stores and read with plain loads: they are small, the end of the producing kernel writes them
+// back from L2 at little cost, and the merge then reads them from the cache hierarchy. Larger
+// partials use nontemporal stores and loads, which keep them from displacing the history.
+template <bool PLAIN, typename T>
+__device__ __forceinline__ T merge_load(const T* p) {
+  if constexpr (PLAIN)
+    return *p;
+  else
+    return __builtin_nontemporal_load(p);
+}
+
+// x combined with the value of lane l ^ 8 (DPP row_ror:8 inside each row of 16 lanes).
+__device__ __forceinline__ float lane_xor8(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x128, 0xf, 0xf, false));
+}
+
+// Reductions over lanes l ^ 16 and l ^ 32 (permlane32_swap, then permlane16_swap). Every lane
+// ends with the same operands in the same order, so all lanes hold identical bits.
+__device__ __forceinline__ float max_over_hi(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+__device__ __forceinline__ float sum_over_hi(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
 // Precision-1 merge (unnormalized fp32 O partials, 256 bytes per row): one wave per query row
-// (lane = threadIdx.x % 64). Lane l = 16 j + c reads 16-byte chunk c (columns 4c + [0, 4)) of
-// split s0 + 4 i + j for i = 0..15, so each load instruction covers 4 splits, and accumulates them
-// weighted by 2^(m_s - M), computed once on lane s and fetched with a shuffle. The 4 lanes of one
-// chunk are summed at the end, and lanes 0..15 store the row.
+// (lane = threadIdx.x % 64). Lane l = 16 j + c reads 16-byte chunk c (columns 4c + [0, 4)) and
+// the (max, sum) of split s0 + 4 i + j for i = 0..15, so each load instruction covers 4 splits,
+// and accumulates them weighted by 2^(m_s - M). Sums over j (lanes 16 and 32 apart) finish the
+// row, and lanes 0..15 store it.
+template <bool PLAIN = false>
 __device__ __forceinline__ void merge_row_f32(const dkv_attn_args& a, int h, int r, int R, int G, int splits,
                                               int active, const float* __restrict__ part_o,
                                               const float2* __restrict__ part_ml) {
   const int lane = threadIdx.x & 63;
   const int64_t base = (int64_t)h * splits * R + r;
   const int j = lane >> 4, c = lane & 15;
-  const float4* rows = reinterpret_cast<const float4*>(part_o);  // 16 chunks of 16 bytes per row
+  const u32x4* rows = reinterpret_cast<const u32x4*>(part_o);  // 16 chunks of 16 bytes per row
+  const merge_f32x2* mls = reinterpret_cast<const merge_f32x2*>(part_ml);
   float M = -INFINITY, L = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
   for (int s0 = 0; s0 < active; s0 += 64) {
     const int cnt = min(64, active - s0);
-    const float2 ml = lane < cnt ? part_ml[base + (int64_t)(s0 + lane) * R] : make_float2(-INFINITY, 0.f);
-    float4 raw[16];
+    merge_f32x2 ml[16];
+    u32x4 raw[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)  // splits past cnt load split cnt - 1 (no branches) and weigh 0
+      ml[i] = merge_load<PLAIN>(mls + base + (int64_t)(s0 + min(4 * i + j, cnt - 1)) * R);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      raw[i] = merge_load<PLAIN>(rows + (base + (int64_t)(s0 + min(4 * i + j, cnt - 1)) * R) * 16 + c);
+    __builtin_amdgcn_sched_barrier(0);  // every load issued before the first wait (one round trip)
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (4 * i + j >= cnt) ml[i].x = -INFINITY;
+    float bm = ml[0].x;
+#pragma unroll
+    for (int i = 1; i < 16; ++i) bm = fmaxf(bm, ml[i].x);
+    bm = fmaxf(max_over_hi(bm), M);
+    // No branch on bm == -inf (no split so far saw a visible key): then every weight and f0 are 0
+    // and the state stays (M, L, acc) = (-inf, 0, 0); a branch would sink the O loads below it.
+    float w[16], lsum = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int sp = 4 * i + j;
-      const u32x4* src = reinterpret_cast<const u32x4*>(rows) + (base + (int64_t)(s0 + sp) * R) * 16 + c;
-      raw[i] = sp < cnt ? __builtin_bit_cast(float4, __builtin_nontemporal_load(src)) : make_float4(0.f, 0.f, 0.f, 0.f);
+      w[i] = ml[i].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml[i].x - bm);
+      lsum = fmaf(ml[i].y, w[i], lsum);
     }
-    float bm = ml.x;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) bm = fmaxf(bm, __shfl_xor(bm, o));
-    bm = fmaxf(bm, M);
-    if (bm == -INFINITY) continue;  // wave-uniform: every split so far saw no visible key
-    const float f = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - bm);
-    float lsum = ml.y * f;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o);
+    lsum = sum_over_hi(lsum);
     const float f0 = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - bm);
     L = fmaf(L, f0, lsum);
 #pragma unroll
     for (int e = 0; e < 4; ++e) acc[e] *= f0;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const float w = __shfl(f, 4 * i + j);  // 0 for splits past cnt
-      acc[0] = fmaf(raw[i].x, w, acc[0]);
-      acc[1] = fmaf(raw[i].y, w, acc[1]);
-      acc[2] = fmaf(raw[i].z, w, acc[2]);
-      acc[3] = fmaf(raw[i].w, w, acc[3]);
+      const float4 v = __builtin_bit_cast(float4, raw[i]);
+      acc[0] = fmaf(v.x, w[i], acc[0]);
+      acc[1] = fmaf(v.y, w[i], acc[1]);
+      acc[2] = fmaf(v.z, w[i], acc[2]);
+      acc[3] = fmaf(v.w, w[i], acc[3]);
     }
     M = bm;
   }
 #pragma unroll
-  for (int o = 16; o < 64; o <<= 1)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) acc[e] += __shfl_xor(acc[e], o);
+  for (int e = 0; e < 4; ++e) acc[e] = sum_over_hi(acc[e]);
   if (j == 0) {  // lanes 0..15 store the row (a guarded store, not an early return: callers loop over rows)
     const float inv = 1.f / L;
     const float v0 = acc[0] * inv, v1 = acc[1] * inv, v2 = acc[2] * inv, v3 = acc[3] * inv;
@@ -69,65 +117,76 @@ __device__ __forceinline__ void merge_row_f32(const dkv_attn_args& a, int h, int
   }
 }
 
-// Precision-0 merge (fp16 O / sum partials, 128 bytes per row in half_slot()
-// order): one wave per query row. Lane l = 8 j + c reads 16-byte chunk c of
-// split s0 + 8 i + j for i = 0..7, so each load instruction covers 8 splits,
-// and accumulates 8 columns weighted by that split's sum * 2^(m_s - M)
-// (fetched from lane s with a shuffle). The 8 lanes of one chunk are summed
-// at the end, and lanes 0..7 store the row.
+// Precision-0 merge (fp16 O / sum partials, 128 bytes per row in half_slot() order): one wave
+// per query row. Lane l = 8 j + c reads 16-byte chunk c and the (max, sum) of split s0 + 8 i + j
+// for i = 0..7, so each load instruction covers 8 splits, and accumulates 8 columns weighted by
+// that split's sum * 2^(m_s - M). Sums over j (lanes 8, 16 and 32 apart) finish the row, and
+// lanes 0..7 store it.
+template <bool PLAIN = false>
 __device__ __forceinline__ void merge_row_half(const dkv_attn_args& a, int h, int r, int R, int G, int splits,
                                                int active, const float* __restrict__ part_o,
                                                const float2* __restrict__ part_ml) {
   const int lane = threadIdx.x & 63;
   const int64_t base = (int64_t)h * splits * R + r;
   const int j = lane >> 3, c = lane & 7;
-  const uint4* rows = reinterpret_cast<const uint4*>(part_o);  // 8 chunks of 16 bytes per row
+  const u32x4* rows = reinterpret_cast<const u32x4*>(part_o);  // 8 chunks of 16 bytes per row
+  const merge_f32x2* mls = reinterpret_cast<const merge_f32x2*>(part_ml);
   float M = -INFINITY, L = 0.f, acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
   for (int s0 = 0; s0 < active; s0 += 64) {
     const int cnt = min(64, active - s0);
-    const float2 ml = lane < cnt ? part_ml[base + (int64_t)(s0 + lane) * R] : make_float2(-INFINITY, 0.f);
-    uint4 raw[8];
+    merge_f32x2 ml[8];
+    u32x4 raw[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)  // splits past cnt load split cnt - 1 (no branches) and weigh 0
+      ml[i] = merge_load<PLAIN>(mls + base + (int64_t)(s0 + min(8 * i + j, cnt - 1)) * R);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      raw[i] = merge_load<PLAIN>(rows + (base + (int64_t)(s0 + min(8 * i + j, cnt - 1)) * R) * 8 + c);
+    __builtin_amdgcn_sched_barrier(0);  // every load issued before the first wait (one round trip)
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (8 * i + j >= cnt) ml[i].x = -INFINITY;
+    float bm = ml[0].x;
+#pragma unroll
+    for (int i = 1; i < 8; ++i) bm = fmaxf(bm, ml[i].x);
+    bm = fmaxf(bm, lane_xor8(bm));
+    bm = fmaxf(max_over_hi(bm), M);
+    // No branch on bm == -inf, as in merge_row_f32.
+    float w[8], lsum = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int s = 8 * i + j;
-      const u32x4* src = reinterpret_cast<const u32x4*>(rows) + (base + (int64_t)(s0 + s) * R) * 8 + c;
-      raw[i] = s < cnt ? __builtin_bit_cast(uint4, __builtin_nontemporal_load(src)) : make_uint4(0, 0, 0, 0);
+      const float f = ml[i].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml[i].x - bm);
+      int ex;
+      const float ls = half_partial_decode(ml[i].y, ex) * f;
+      w[i] = ex ? __builtin_amdgcn_ldexpf(ls, ex) : ls;  // weight of the stored O / sum / 2^ex
+      lsum += ls;
     }
-    float bm = ml.x;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) bm = fmaxf(bm, __shfl_xor(bm, o));
-    bm = fmaxf(bm, M);
-    if (bm == -INFINITY) continue;  // wave-uniform: every split so far saw no visible key
-    const float f = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - bm);
-    int ex;
-    float lsum = half_partial_decode(ml.y, ex) * f;
-    const float wsplit = ex ? __builtin_amdgcn_ldexpf(lsum, ex) : lsum;  // weight of the stored O / sum / 2^ex
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o);
+    lsum += lane_xor8(lsum);
+    lsum = sum_over_hi(lsum);
     const float f0 = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - bm);
     L = fmaf(L, f0, lsum);
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] *= f0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float w = __shfl(wsplit, 8 * i + j);  // 0 for splits past cnt
       const uint32_t q[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const _Float16 lo = __builtin_bit_cast(_Float16, (uint16_t)(q[e] & 0xffffu));
         const _Float16 hi = __builtin_bit_cast(_Float16, (uint16_t)(q[e] >> 16));
-        acc[2 * e] = fmaf((float)lo, w, acc[2 * e]);
-        acc[2 * e + 1] = fmaf((float)hi, w, acc[2 * e + 1]);
+        acc[2 * e] = fmaf((float)lo, w[i], acc[2 * e]);
+        acc[2 * e + 1] = fmaf((float)hi, w[i], acc[2 * e + 1]);
       }
     }
     M = bm;
   }
 #pragma unroll
-  for (int o = 8; o < 64; o <<= 1)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], o);
+  for (int e = 0; e < 8; ++e) {
+    acc[e] += lane_xor8(acc[e]);
+    acc[e] = sum_over_hi(acc[e]);
+  }
   if (j == 0) {  // lanes 0..7 store the row (a guarded store, not an early return: callers loop over rows)
     const float inv = 1.f / L;
     const int gq = r / a.nq, m = r - gq * a.nq;
