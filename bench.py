@@ -535,16 +535,18 @@ def timeline(kind, past, nq, rotate, path=None):
     bits = bit_schedule(past, (past + TILE - 1) // TILE)
     path = path or ('auto' if kind == 'mfma' else kind)
     replay, nbytes, keep = attention_setup(past, rotate, bits, nq=nq, seed=past + nq, path=path)
-    ms = time_launches(replay, 10, 2) / keep['rotate']
-    torch.cuda.synchronize()
 
-    def read(name):
+    def read(name):  # the stamps, which the library then clears
         f = getattr(lib, name)
         f.restype, f.argtypes = ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64]
         stamps = np.zeros((1 << 14) * TIMELINE_STAMPS, dtype=np.uint64)
         _lib.check(f(stamps.ctypes.data, stamps.nbytes), name)
         t = stamps.reshape(-1, TIMELINE_STAMPS).astype(np.int64)
         return t[t[:, 0] > 0]
+    torch.cuda.synchronize()
+    read('dkv_timeline_' + kind), read('dkv_timeline_combine')  # no stamps of earlier, larger grids
+    ms = time_launches(replay, 10, 2) / keep['rotate']
+    torch.cuda.synchronize()
     t = read('dkv_timeline_' + kind)
     merge = read('dkv_timeline_combine')
     t0 = t[:, 0].min()

@@ -568,9 +568,6 @@ int dkv_attend_noalloc(const dkv_attn_args* args, void* stream) {
 }  // extern "C"
 
 #ifdef DKV_TIMELINE
-// Timeline build only: copies the merge kernels' stamps of the last launch.
-extern "C" int dkv_timeline_combine(void* host, int64_t bytes) {
-  const int64_t n = sizeof(dkv::tl_comb) < (uint64_t)bytes ? sizeof(dkv::tl_comb) : bytes;
-  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(dkv::tl_comb), n, 0, hipMemcpyDeviceToHost);
-}
+// Timeline build only: copies the merge kernels' stamps of the last launch and clears them.
+extern "C" int dkv_timeline_combine(void* host, int64_t bytes) { return dkv::timeline_take(dkv::tl_comb, host, bytes); }
 #endif

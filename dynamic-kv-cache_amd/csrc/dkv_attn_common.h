@@ -12,8 +12,8 @@ constexpr float LOG2E = 1.4426950408889634f;
 // Timeline probe, a build option (-DDKV_TIMELINE; off in the library build):
 // lane 0 of each workgroup records wall_clock64() (a 100 MHz counter shared by
 // all CUs) at numbered points of a kernel into its source file's device array,
-// which that build's dkv_timeline_*() export copies out. Used to see where a
-// launch's time goes (which memory round trips sit on the critical path).
+// which that build's dkv_timeline_*() export copies out and clears. Used to see
+// where a launch's time goes (which memory round trips sit on the critical path).
 #ifdef DKV_TIMELINE
 constexpr int TL_EVENTS = 10;  // 8 and 9: the in-kernel merge build's
 constexpr int TL_SLOTS = 1 << 14;  // workgroups recorded per launch
@@ -24,6 +24,15 @@ constexpr int TL_SLOTS = 1 << 14;  // workgroups recorded per launch
       if (tl_wg < TL_SLOTS) buf[tl_wg * TL_EVENTS + (ev)] = wall_clock64();                    \
     }                                                                                          \
   } while (0)
+// Copies a kernel's stamp array to the host and zeroes it, so that a later read holds only the
+// workgroups of later launches (a smaller grid leaves no stale slots behind).
+inline int timeline_take(const uint64_t (&stamps)[TL_SLOTS * TL_EVENTS], void* host, int64_t bytes) {
+  const int64_t n = (int64_t)sizeof(stamps) < bytes ? (int64_t)sizeof(stamps) : bytes;
+  hipError_t e = hipMemcpyFromSymbol(host, HIP_SYMBOL(stamps), n, 0, hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return (int)e;
+  static const uint64_t zeros[TL_SLOTS * TL_EVENTS] = {};
+  return (int)hipMemcpyToSymbol(HIP_SYMBOL(stamps), zeros, sizeof(stamps), 0, hipMemcpyHostToDevice);
+}
 #else
 #define DKV_TL(buf, ev) \
   do {                  \

@@ -718,9 +718,6 @@ int launch_attn_mfma(const dkv_attn_args& a, const Plan& p, float* part_o, float
 }  // namespace dkv
 
 #ifdef DKV_TIMELINE
-// Timeline build only: copies the frame-chunk kernel's stamps of the last launch.
-extern "C" int dkv_timeline_mfma(void* host, int64_t bytes) {
-  const int64_t n = sizeof(dkv::tl_mfma) < (uint64_t)bytes ? sizeof(dkv::tl_mfma) : bytes;
-  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(dkv::tl_mfma), n, 0, hipMemcpyDeviceToHost);
-}
+// Timeline build only: copies the frame-chunk kernel's stamps of the last launch and clears them.
+extern "C" int dkv_timeline_mfma(void* host, int64_t bytes) { return dkv::timeline_take(dkv::tl_mfma, host, bytes); }
 #endif

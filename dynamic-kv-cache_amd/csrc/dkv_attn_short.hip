@@ -411,9 +411,6 @@ int launch_attn_short(const dkv_attn_args& a, const Plan& p, float* part_o, floa
 }  // namespace dkv
 
 #ifdef DKV_TIMELINE
-// Timeline build only: copies the short-chunk kernel's stamps of the last launch.
-extern "C" int dkv_timeline_short(void* host, int64_t bytes) {
-  const int64_t n = sizeof(dkv::shortpath::tl_short) < (uint64_t)bytes ? sizeof(dkv::shortpath::tl_short) : bytes;
-  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(dkv::shortpath::tl_short), n, 0, hipMemcpyDeviceToHost);
-}
+// Timeline build only: copies the short-chunk kernel's stamps of the last launch and clears them.
+extern "C" int dkv_timeline_short(void* host, int64_t bytes) { return dkv::timeline_take(dkv::shortpath::tl_short, host, bytes); }
 #endif
