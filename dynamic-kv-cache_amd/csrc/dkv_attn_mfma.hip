@@ -136,32 +136,48 @@ __device__ __forceinline__ void part_store(const T& v, T* p) {
 // which spreads the rows a dequantizing wave reads over all banks.
 __device__ __forceinline__ int padded(int off) { return off + ((off >> 7) << 4); }
 
-// 8 fp32 values q*s + a of row r, columns [8*db, 8*db + 8), of a 4/8-bit raw
-// sub-block in LDS (multiply and add rounded separately, as the reference's unpack).
-__device__ __forceinline__ void dequant8(const uint8_t* raw, int bits, int rows, int r, int db, float* x) {
-  const float2 as = *reinterpret_cast<const float2*>(raw + padded(rows * (int)row_bytes(bits) + 8 * r));
-  float q[8];
-  if (bits == 4) {
-    const uint32_t w = *reinterpret_cast<const uint32_t*>(raw + padded(r * 32 + db * 4));
-    uint32_t ev = w & 0x0f0f0f0fu, od = (w >> 4) & 0x0f0f0f0fu;  // even / odd elements
+// 8 fp32 values q*s + a of rows r0 and r0 + 1 (r0 even), columns [8*db, 8*db + 8), of a 4/8-bit
+// raw sub-block in LDS (multiply and add rounded separately, as the reference's unpack). Every
+// LDS read (the two rows' codes and their (offset, scale) pairs, which sit side by side) is
+// issued before the first use, so a unit's dequantization waits on one LDS round trip (with one
+// row per call and the width branch between the reads, the compiler waited on each row's reads
+// in turn).
+template <int BITS>
+__device__ __forceinline__ void dequant_pair(const uint8_t* raw, int rows, int r0, int db, float* x0, float* x1) {
+  constexpr int RB = BITS == 4 ? 32 : 64;
+  const float4 as = *reinterpret_cast<const float4*>(raw + padded(rows * RB + 8 * r0));  // (a0, s0, a1, s1)
+  float q0[8], q1[8];
+  if (BITS == 4) {
+    const uint32_t w0 = *reinterpret_cast<const uint32_t*>(raw + padded(r0 * 32 + db * 4));
+    const uint32_t w1 = *reinterpret_cast<const uint32_t*>(raw + padded(r0 * 32 + 32 + db * 4));
+    uint32_t ev0 = w0 & 0x0f0f0f0fu, od0 = (w0 >> 4) & 0x0f0f0f0fu;  // even / odd elements
+    uint32_t ev1 = w1 & 0x0f0f0f0fu, od1 = (w1 >> 4) & 0x0f0f0f0fu;
     // Opaque to the optimizer (no instruction), which would otherwise fold each byte back into a
     // nibble extract of w (v_bfe, then a convert) instead of one v_cvt_f32_ubyteN per element.
-    asm("" : "+v"(ev), "+v"(od));
+    asm("" : "+v"(ev0), "+v"(od0), "+v"(ev1), "+v"(od1));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      q[2 * i] = (float)((ev >> (8 * i)) & 255u);
-      q[2 * i + 1] = (float)((od >> (8 * i)) & 255u);
+      q0[2 * i] = (float)((ev0 >> (8 * i)) & 255u);
+      q0[2 * i + 1] = (float)((od0 >> (8 * i)) & 255u);
+      q1[2 * i] = (float)((ev1 >> (8 * i)) & 255u);
+      q1[2 * i + 1] = (float)((od1 >> (8 * i)) & 255u);
     }
   } else {
-    const uint2 w = *reinterpret_cast<const uint2*>(raw + padded(r * 64 + db * 8));
+    const uint2 w0 = *reinterpret_cast<const uint2*>(raw + padded(r0 * 64 + db * 8));
+    const uint2 w1 = *reinterpret_cast<const uint2*>(raw + padded(r0 * 64 + 64 + db * 8));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      q[i] = (float)((w.x >> (8 * i)) & 255u);
-      q[4 + i] = (float)((w.y >> (8 * i)) & 255u);
+      q0[i] = (float)((w0.x >> (8 * i)) & 255u);
+      q0[4 + i] = (float)((w0.y >> (8 * i)) & 255u);
+      q1[i] = (float)((w1.x >> (8 * i)) & 255u);
+      q1[4 + i] = (float)((w1.y >> (8 * i)) & 255u);
     }
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) x[i] = __fadd_rn(__fmul_rn(q[i], as.y), as.x);
+  for (int i = 0; i < 8; ++i) {
+    x0[i] = __fadd_rn(__fmul_rn(q0[i], as.y), as.x);
+    x1[i] = __fadd_rn(__fmul_rn(q1[i], as.w), as.z);
+  }
 }
 
 // Row r, columns [8*db, 8*db + 8), of a bf16 raw sub-block (16-bit tiles and chunk pieces).
@@ -169,10 +185,23 @@ __device__ __forceinline__ uint4 bf16_row8(const uint8_t* raw, int r, int db) {
   return *reinterpret_cast<const uint4*>(raw + padded(r * 128 + db * 16));
 }
 
-// One 16-byte piece of K (threads 0..511 -> pieces 0..511) and one of V;
-// threads 512 and up load nothing (every sub-block is at most 512 pieces).
-__device__ __forceinline__ void raw_load(const dkv_attn_args& a, const Unit& un, int h, uint4& wk, uint4& wv) {
-  const int p = threadIdx.x;
+// Loader index of a thread: which 512 threads load, stage and dequantize a unit. With two query
+// blocks per wave (every wave computes) they are waves 0-7. With one (decode steps, short
+// chunks: only query block 0 of each key group, waves 0 and 6, computes) they are waves 1-5, 7,
+// 8 and 10, so the computing waves work on one unit while the others dequantize the next
+// rather than after it (decode at past 8128: 10.9 -> 10.7 us; the frame chunk ran 0.3 us slower
+// with this order). Wave w holds slot SLOTS >> 4w & 15 (15: no slot); waves 9 and 11 idle so
+// that each SIMD keeps two loading waves (wave w runs on SIMD w mod 4).
+template <int NBW>
+__device__ __forceinline__ int loader_index(int wave, int lane) {
+  constexpr uint64_t SLOTS = NBW == 1 ? 0xF7F65F43210FULL : 0xFFFF76543210ULL;
+  const int slot = (int)((SLOTS >> (4 * wave)) & 15);
+  return slot == 15 ? MF_LOADERS + lane : slot * 64 + lane;
+}
+
+// One 16-byte piece of K (loader index p = 0..511 -> pieces 0..511) and one of V;
+// threads with p >= 512 load nothing (every sub-block is at most 512 pieces).
+__device__ __forceinline__ void raw_load(const dkv_attn_args& a, const Unit& un, int h, int p, uint4& wk, uint4& wv) {
   wk = wv = make_uint4(0, 0, 0, 0);
   if (un.chunk) {
     const int row = p >> 3, c = p & 7;
@@ -257,6 +286,7 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
   const int R = G * a.nq;
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int lt = loader_index<NBW>(wave, lane);
   const int kg = wave / KG_WAVES, w = wave - kg * KG_WAVES;  // key group, wave within the group
   const int col = lane & 15, g = lane >> 4;
   if (split >= active) return;  // graph replay over a shorter history than the launch bound
@@ -308,10 +338,10 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
   // cover 32 consecutive words of a V^T row). bf16 rows (16-bit tiles, chunk
   // pieces) are copied or byte-permuted without a float round trip.
   auto dequant = [&](const Unit& un, int st, int b) {
-    if (t >= MF_LOADERS) return;
-    const bool is_v = t >= 256;
-    const int kp = is_v ? (t & 31) : ((t & 255) >> 3);
-    const int db = is_v ? ((t & 255) >> 5) : (t & 7);
+    if (lt >= MF_LOADERS) return;
+    const bool is_v = lt >= 256;
+    const int kp = is_v ? (lt & 31) : ((lt & 255) >> 3);
+    const int db = is_v ? ((lt & 255) >> 5) : (lt & 7);
     const int r0 = 2 * kp, r1 = r0 + 1;
     const bool ok0 = r0 < un.valid, ok1 = r1 < un.valid;
     const uint8_t* raw = raw_buf(st, is_v ? 1 : 0);
@@ -335,20 +365,16 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
       return;
     }
     float x0[8], x1[8];
-    if (un.valid == TILE) {  // wave-uniform: every row of a full tile is valid
-      dequant8(raw, un.bits, un.rows, r0, db, x0);
-      dequant8(raw, un.bits, un.rows, r1, db, x1);
-    } else {
+    if (un.bits == 4) dequant_pair<4>(raw, un.rows, r0, db, x0, x1);
+    else dequant_pair<8>(raw, un.rows, r0, db, x0, x1);
+    if (un.valid != TILE) {  // wave-uniform: every row of a full tile is valid
       // rows past `valid` hold stale staging bytes; they become zeros (P is 0 there, and a
       // stale NaN would still poison P.V)
-      if (ok0) dequant8(raw, un.bits, un.rows, r0, db, x0);
-      else
 #pragma unroll
-        for (int i = 0; i < 8; ++i) x0[i] = 0.f;
-      if (ok1) dequant8(raw, un.bits, un.rows, r1, db, x1);
-      else
-#pragma unroll
-        for (int i = 0; i < 8; ++i) x1[i] = 0.f;
+      for (int i = 0; i < 8; ++i) {
+        x0[i] = ok0 ? x0[i] : 0.f;
+        x1[i] = ok1 ? x1[i] : 0.f;
+      }
     }
     if (!is_v) {
       uint16_t* k_hi = tile(b, 0);
@@ -383,8 +409,9 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
     }
   };
 
-  // MFMA work of one dequantized unit held in tile set b.
-  auto compute = [&](const Unit& un, int b) {
+  // MFMA work of one dequantized unit held in tile set b; `first` marks the workgroup's first
+  // unit, before which the running maxima are -inf and the accumulators zero.
+  auto compute = [&](const Unit& un, int b, bool first) {
     if (!wave_on) return;
     const uint16_t* k_hi = tile(b, 0);
     const uint16_t* v_hi = tile(b, 1);
@@ -448,7 +475,13 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
       // Lazy rescaling: a wave moves its running maxima (and rescales its
       // accumulators) only when some column's max grew by more than
       // rescale_log2; otherwise p = 2^(x - m_run) <= 2^rescale_log2.
-      if (__builtin_amdgcn_ballot_w64(mcand > m_run[nb] + rescale_log2<PREC>())) {
+      if (PREC == 0 && first) {
+        // nothing accumulated yet: the maxima move without rescaling zeros (the branch below
+        // would multiply them by 0; at precision 0 and three units per workgroup it runs in most
+        // units; at precision 1 it rarely runs past the first unit, and the separate first-unit
+        // path made the kernel spill)
+        m_run[nb] = max_nn(m_run[nb], mcand);
+      } else if (__builtin_amdgcn_ballot_w64(mcand > m_run[nb] + rescale_log2<PREC>())) {
         const float mnew = max_nn(m_run[nb], mcand);
         const float alpha = mnew == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run[nb] - mnew);
         m_run[nb] = mnew;
@@ -514,19 +547,19 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
   asm volatile("" ::"v"(win.x), "v"(win.y), "v"(win.z), "v"(win.w));
   auto unit = [&](int rel) { return unit_at(a, hs, u0 + rel, rel, h, win, in_args); };
   auto stage = [&](int st, const uint4& wk, const uint4& wv) {
-    if (t >= MF_LOADERS) return;  // a raw sub-block is at most MF_LOADERS pieces of 16 bytes
-    *reinterpret_cast<uint4*>(raw_buf(st, 0) + padded(16 * t)) = wk;
-    *reinterpret_cast<uint4*>(raw_buf(st, 1) + padded(16 * t)) = wv;
+    if (lt >= MF_LOADERS) return;  // a raw sub-block is at most MF_LOADERS pieces of 16 bytes
+    *reinterpret_cast<uint4*>(raw_buf(st, 0) + padded(16 * lt)) = wk;
+    *reinterpret_cast<uint4*>(raw_buf(st, 1) + padded(16 * lt)) = wv;
   };
   uint4 wk, wv, wk0, wv0, wk2, wv2;
-  if (n > 0) raw_load(a, unit(0), h, wk0, wv0);
-  if (n > 1) raw_load(a, unit(1), h, wk, wv);  // in flight while unit 0 is staged
+  if (n > 0) raw_load(a, unit(0), h, lt, wk0, wv0);
+  if (n > 1) raw_load(a, unit(1), h, lt, wk, wv);  // in flight while unit 0 is staged
   // With two query blocks per wave (frame chunks, candidate batches) unit 2's loads go out at
   // once too, not after unit 0 is staged and dequantized (past 1024 11.60 -> 11.37 us, 4096
   // 13.98 -> 13.83). With one (decode steps), whose units compute little, the larger first
   // burst delayed unit 0 more than it saved (11.68 -> 11.83 us at past 8128).
   constexpr bool early2 = NBW == 2;
-  if (early2 && n > 2) raw_load(a, unit(2), h, wk2, wv2);
+  if (early2 && n > 2) raw_load(a, unit(2), h, lt, wk2, wv2);
   if (n > 0) stage(0, wk0, wv0);
   // unit 0's load registers are settled on every path before the loop (the compiler does not
   // tie the two n > 0 tests together and would otherwise wait on them inside the loop, where a
@@ -537,7 +570,7 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
   if (n > 0) dequant(unit(0), 0, 0);
   DKV_TL(tl_mfma, 2);
   if (n > 1) stage(1, wk, wv);
-  if (!early2 && n > 2) raw_load(a, unit(2), h, wk, wv);
+  if (!early2 && n > 2) raw_load(a, unit(2), h, lt, wk, wv);
   for (int i = 0; i < n; ++i) {
     __syncthreads();
     if (i + 1 < n) dequant(unit(i + 1), (i + 1) & 1, (i + 1) & 1);
@@ -546,9 +579,9 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
         stage(0, wk2, wv2);
       else
         stage(i & 1, wk, wv);
-      if (i + 3 < n) raw_load(a, unit(i + 3), h, wk, wv);
+      if (i + 3 < n) raw_load(a, unit(i + 3), h, lt, wk, wv);
     }
-    compute(unit(i), i & 1);
+    compute(unit(i), i & 1, i == 0);
     if (i == 0) DKV_TL(tl_mfma, 3);
   }
   DKV_TL(tl_mfma, 4);
