@@ -148,6 +148,14 @@ __device__ __forceinline__ void pack_loaded(const dkv_pack_job& j, int kv, int h
   // Arena stores are nontemporal: lines written with plain stores stay dirty in
   // L2 and the end of the kernel writes all of them back before it completes.
   if (BITS == 16) {
+    if (one_tile && nrows == WAVE_ROWS) {  // a full slice in one tile: no per-row tests
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int r = 8 * i + (lane >> 3);
+        __builtin_nontemporal_store(w[i], reinterpret_cast<u32x4*>(d0.payload + r * 128 + 16 * c));
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int r = 8 * i + (lane >> 3);
@@ -200,7 +208,8 @@ __device__ __forceinline__ void pack_loaded(const dkv_pack_job& j, int kv, int h
     }
     return;
   }
-  if (valid) __builtin_nontemporal_store((f32x2_t{a, s}), reinterpret_cast<f32x2_t*>(d0.meta + lane));
+  // (nrows == WAVE_ROWS: every lane's row is valid; the compiler cannot tell that from `valid`)
+  if (valid || nrows == WAVE_ROWS) __builtin_nontemporal_store((f32x2_t{a, s}), reinterpret_cast<f32x2_t*>(d0.meta + lane));
   // Packed rows back through LDS (the wave's own region, already read), then
   // contiguous 16-byte stores: RB bytes per row, rows back to back.
   wave_sync_lds();
@@ -212,7 +221,7 @@ __device__ __forceinline__ void pack_loaded(const dkv_pack_job& j, int kv, int h
 #pragma unroll
   for (int i = 0; i < RB / 16; ++i) {
     const int off = 16 * (lane + 64 * i);
-    if (off < bytes)
+    if (nrows == WAVE_ROWS || off < bytes)
       __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(lds + off), reinterpret_cast<u32x4*>(d0.payload + off));
   }
 }
@@ -226,12 +235,25 @@ __device__ __forceinline__ void pack_wave(const dkv_pack_job& j, int kv, int hea
                                  : static_cast<const uint16_t*>(j.v) + head * j.v_head_stride;
   const int64_t ts = kv == 0 ? j.k_tok_stride : j.v_tok_stride;
   const int nrows = min(WAVE_ROWS, j.n - tok0);
+  // The job's K/V pointers come from memory, so the compiler cannot tell they are global and
+  // would emit flat loads; a full slice (every slice but a partial append's last) loads all
+  // rows with no per-row test, so the eight loads go out back to back (72.9 -> 72.5 us for the
+  // 32-layer, 96-frame volume).
+  typedef const __attribute__((address_space(1))) u32x4 global_u32x4;
   u32x4 w[8];
+  if (nrows == WAVE_ROWS) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int r = 8 * i + (lane >> 3);
-    w[i] = r < nrows ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + (tok0 + r) * ts + 8 * c))
-                     : u32x4{0, 0, 0, 0};
+    for (int i = 0; i < 8; ++i) {
+      const int r = 8 * i + (lane >> 3);
+      w[i] = __builtin_nontemporal_load((global_u32x4*)(base + (tok0 + r) * ts + 8 * c));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = 8 * i + (lane >> 3);
+      w[i] = r < nrows ? __builtin_nontemporal_load((global_u32x4*)(base + (tok0 + r) * ts + 8 * c))
+                       : u32x4{0, 0, 0, 0};
+    }
   }
   pack_loaded<BITS>(j, kv, head, tok0, nrows, w, arena, layers, heads, lds);
 }
