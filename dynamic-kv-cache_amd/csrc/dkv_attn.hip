@@ -393,6 +393,7 @@ static Plan make_plan(const dkv_attn_args& a) {
     p.rows_per_group = 16 * ((blocks + p.row_groups - 1) / p.row_groups);
   }
   p.units = a.n_tiles + (a.nq + TILE - 1) / TILE;
+  p.small = a.path == 0 && p.precision == 0 && R <= MFMA_SMALL_ROWS;
   int splits = a.splits;
   p.cap = 0;
   if (splits <= 0) {
@@ -406,7 +407,7 @@ static Plan make_plan(const dkv_attn_args& a) {
       // would take a second round for a single workgroup); balanced over the history. A launch
       // that reads its history from a device step pair (graph replays) is sized for the cap,
       // the most splits any history runs.
-      p.cap = p.path == 2 ? num_cus() / per : (2 * num_cus() + per - 1) / per;
+      p.cap = p.path == 2 ? (p.small ? MFMA_SMALL_PER_CU : 1) * num_cus() / per : (2 * num_cus() + per - 1) / per;
       if (p.cap < 1) p.cap = 1;
       splits = a.step ? p.cap : balanced_splits(p.units, p.cap);
     }

@@ -206,6 +206,7 @@ struct Plan {
   int cap;        // default split cap (0: the caller's explicit split count)
   int fused;      // the in-kernel merge build: the frame-chunk kernel merges its own splits
   int plain_parts;  // MFMA split partials of the one-block-per-wave variant: plain stores and loads
+  int small;      // MFMA decode-step variant: 4-wave workgroups, four per CU (MFMA_SMALL_ROWS)
   int64_t part_o_bytes, part_ml_bytes;
 };
 
@@ -246,6 +247,13 @@ __device__ __forceinline__ int short_runtime_plan(const dkv_attn_args& a, Hist& 
   return max(1, min(nwg, want));
 }
 constexpr int MFMA_ROWS = 192;  // query rows per MFMA-path workgroup (6 waves x 2 blocks x 16)
+// The auto path's decode-step variant of the MFMA kernel (precision 0, at most this many query rows
+// per KV head): 4-wave workgroups with one buffer of raw bytes and tiles, four per CU.
+constexpr int MFMA_SMALL_ROWS = 32;
+// Workgroups of it per CU (36 KB of LDS each). Precision 1 needs 54 KB (hi and lo tiles), two
+// per CU, and two units per workgroup ran slower than the 12-wave kernel (12.24 vs 11.24 us for
+// a decode step at past 8128), so only precision 0 takes this variant.
+constexpr int MFMA_SMALL_PER_CU = 4;
 
 // Precision-0 split partials hold O / sum in fp16, 64 values per row (128
 // bytes) in the order the MFMA kernel's lanes store them: the lane of 16-byte

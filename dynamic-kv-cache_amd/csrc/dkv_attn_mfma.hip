@@ -13,6 +13,12 @@
 // separate online-softmax states and merge through LDS after the last unit.
 // Threads 0..511 stage and dequantize the units; the others only compute.
 //
+// Decode steps at precision 0 (at most 32 query rows per KV head) take the SMALL variant instead:
+// 4 waves (two key groups of 2), every thread loading and dequantizing two 16-byte pieces of K
+// and of V per unit, one buffer of raw bytes and tiles (36 KB of LDS), four workgroups per CU, so
+// the default plan gives each workgroup one 64-key unit: after the history's burst of loads each
+// workgroup has one unit left to do rather than three.
+//
 // Per unit:
 //   1. the raw K and V sub-blocks (codes + (offset, scale) pairs, or bf16 rows)
 //      are copied to LDS with one 16-byte load per thread each;
@@ -258,8 +264,12 @@ static __device__ uint64_t tl_mfma[TL_SLOTS * TL_EVENTS];
 
 // ARGT: the history's tile descriptors come in the argument block (first parameter ArgTiles)
 // rather than from the device table (first parameter NoArgTiles).
-template <int PREC, int NBW, bool ARGT>
-__global__ void __launch_bounds__(MF_THREADS)
+// SMALL: the decode-step variant (precision 0, at most two query blocks per KV head): 4 waves in
+// two key groups of 2, every thread loads and dequantizes two pieces of each unit, one buffer of
+// raw bytes and tiles (36 KB of LDS), so four workgroups share a CU and the default plan gives
+// each workgroup one unit of the history.
+template <int PREC, int NBW, bool ARGT, bool SMALL>
+__global__ void __launch_bounds__(SMALL ? 256 : MF_THREADS, SMALL ? MFMA_SMALL_PER_CU : 3)
 attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dkv_attn_args a, int units,
                  int splits, int cap, int rpg, float* __restrict__ part_o, float2* __restrict__ part_ml
 #if DKV_INKERNEL_MERGE
@@ -269,14 +279,20 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
   // LDS: two raw stages of (K, V) sub-blocks and two sets of bf16 tiles
   // (K, V^T, and for PREC 1 their lo parts). After the last unit the same
   // bytes hold the key-group merge (O rows, then (max, sum) pairs).
+  constexpr int KGW = SMALL ? 2 : KG_WAVES;  // waves per key group
+  constexpr int NST = SMALL ? 1 : 2;          // raw stages and tile sets
+  constexpr int PN = SMALL ? 2 : 1;           // 16-byte pieces of K and of V a loading thread takes
+  constexpr int MROWS = KGW * 16 * NBW;       // query rows of one key group's blocks
   constexpr int NT = PREC ? 4 : 2;
-  constexpr int RAW_BYTES = 2 * 2 * RAWP;
+  constexpr int RAW_BYTES = NST * 2 * RAWP;
   constexpr int TILE_BYTES = 64 * KS * 2;
-  constexpr int SMEM = RAW_BYTES + 2 * NT * TILE_BYTES;
-  static_assert(SMEM >= MFMA_ROWS * MRG_STRIDE * 4 + MFMA_ROWS * 8, "merge buffer must fit");
+  constexpr int SMEM = RAW_BYTES + NST * NT * TILE_BYTES;
+  static_assert(SMEM >= MROWS * MRG_STRIDE * 4 + MROWS * 8, "merge buffer must fit");
   __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
-  auto raw_buf = [&](int st, int kv) { return smem + (st * 2 + kv) * RAWP; };
-  auto tile = [&](int b, int which) { return reinterpret_cast<uint16_t*>(smem + RAW_BYTES + (b * NT + which) * TILE_BYTES); };
+  auto raw_buf = [&](int st, int kv) { return smem + ((NST > 1 ? st : 0) * 2 + kv) * RAWP; };
+  auto tile = [&](int b, int which) {
+    return reinterpret_cast<uint16_t*>(smem + RAW_BYTES + ((NST > 1 ? b : 0) * NT + which) * TILE_BYTES);
+  };
 
   DKV_TL(tl_mfma, 0);
   Hist hs;
@@ -286,8 +302,8 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
   const int R = G * a.nq;
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int lt = loader_index<NBW>(wave, lane);
-  const int kg = wave / KG_WAVES, w = wave - kg * KG_WAVES;  // key group, wave within the group
+  const int lt = SMALL ? t : loader_index<NBW>(wave, lane);  // SMALL: pieces lt and lt + 256
+  const int kg = wave / KGW, w = wave - kg * KGW;  // key group, wave within the group
   const int col = lane & 15, g = lane >> 4;
   if (split >= active) return;  // graph replay over a shorter history than the launch bound
   DKV_TL(tl_mfma, 7);           // the argument block (and any step pair) has arrived
@@ -304,7 +320,7 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
   int qlo[NBW], qhi[NBW];
 #pragma unroll
   for (int nb = 0; nb < NBW; ++nb) {
-    const int r = r0 + (w + KG_WAVES * nb) * 16 + col;
+    const int r = r0 + (w + KGW * nb) * 16 + col;
     Pack8 q0, q1;
     q0.u = q1.u = make_uint4(0, 0, 0, 0);
     qlo[nb] = 0;
@@ -337,11 +353,11 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
   // 256..511 build V^T (kp fastest, so the 4-byte stores of one instruction
   // cover 32 consecutive words of a V^T row). bf16 rows (16-bit tiles, chunk
   // pieces) are copied or byte-permuted without a float round trip.
-  auto dequant = [&](const Unit& un, int st, int b) {
-    if (lt >= MF_LOADERS) return;
-    const bool is_v = lt >= 256;
-    const int kp = is_v ? (lt & 31) : ((lt & 255) >> 3);
-    const int db = is_v ? ((lt & 255) >> 5) : (lt & 7);
+  auto dequant_piece = [&](const Unit& un, int st, int b, int q) {
+    if (q >= MF_LOADERS) return;
+    const bool is_v = q >= 256;
+    const int kp = is_v ? (q & 31) : ((q & 255) >> 3);
+    const int db = is_v ? ((q & 255) >> 5) : (q & 7);
     const int r0 = 2 * kp, r1 = r0 + 1;
     const bool ok0 = r0 < un.valid, ok1 = r1 < un.valid;
     const uint8_t* raw = raw_buf(st, is_v ? 1 : 0);
@@ -407,6 +423,11 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
               pk_bf16(x0[i] - bf16_lo_f(hv), x1[i] - bf16_hi_f(hv));
       }
     }
+  };
+  // A loading thread's pieces of a unit: lt (and lt + 256 in SMALL, K then V^T).
+  auto dequant = [&](const Unit& un, int st, int b) {
+#pragma unroll
+    for (int i = 0; i < PN; ++i) dequant_piece(un, st, b, lt + 256 * i);
   };
 
   // MFMA work of one dequantized unit held in tile set b; `first` marks the workgroup's first
@@ -546,43 +567,76 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
   // cannot place before the loop lands inside it, where it also waits for the prefetches in flight.
   asm volatile("" ::"v"(win.x), "v"(win.y), "v"(win.z), "v"(win.w));
   auto unit = [&](int rel) { return unit_at(a, hs, u0 + rel, rel, h, win, in_args); };
-  auto stage = [&](int st, const uint4& wk, const uint4& wv) {
-    if (lt >= MF_LOADERS) return;  // a raw sub-block is at most MF_LOADERS pieces of 16 bytes
-    *reinterpret_cast<uint4*>(raw_buf(st, 0) + padded(16 * lt)) = wk;
-    *reinterpret_cast<uint4*>(raw_buf(st, 1) + padded(16 * lt)) = wv;
+  // A thread's raw bytes of one unit: PN pieces of K and of V.
+  struct Raw {
+    uint4 k[PN], v[PN];
   };
-  uint4 wk, wv, wk0, wv0, wk2, wv2;
-  if (n > 0) raw_load(a, unit(0), h, lt, wk0, wv0);
-  if (n > 1) raw_load(a, unit(1), h, lt, wk, wv);  // in flight while unit 0 is staged
-  // With two query blocks per wave (frame chunks, candidate batches) unit 2's loads go out at
-  // once too, not after unit 0 is staged and dequantized (past 1024 11.60 -> 11.37 us, 4096
-  // 13.98 -> 13.83). With one (decode steps), whose units compute little, the larger first
-  // burst delayed unit 0 more than it saved (11.68 -> 11.83 us at past 8128).
-  constexpr bool early2 = NBW == 2;
-  if (early2 && n > 2) raw_load(a, unit(2), h, lt, wk2, wv2);
-  if (n > 0) stage(0, wk0, wv0);
-  // unit 0's load registers are settled on every path before the loop (the compiler does not
-  // tie the two n > 0 tests together and would otherwise wait on them inside the loop, where a
-  // wait also drains the prefetches in flight)
-  asm volatile("" ::"v"(wk0.x), "v"(wk0.y), "v"(wk0.z), "v"(wk0.w), "v"(wv0.x), "v"(wv0.y), "v"(wv0.z), "v"(wv0.w));
-  DKV_TL(tl_mfma, 1);
-  __syncthreads();
-  if (n > 0) dequant(unit(0), 0, 0);
-  DKV_TL(tl_mfma, 2);
-  if (n > 1) stage(1, wk, wv);
-  if (!early2 && n > 2) raw_load(a, unit(2), h, lt, wk, wv);
-  for (int i = 0; i < n; ++i) {
-    __syncthreads();
-    if (i + 1 < n) dequant(unit(i + 1), (i + 1) & 1, (i + 1) & 1);
-    if (i + 2 < n) {
-      if (early2 && i == 0)
-        stage(0, wk2, wv2);
-      else
-        stage(i & 1, wk, wv);
-      if (i + 3 < n) raw_load(a, unit(i + 3), h, lt, wk, wv);
+  auto load = [&](int rel, Raw& r) {
+#pragma unroll
+    for (int i = 0; i < PN; ++i) raw_load(a, unit(rel), h, lt + 256 * i, r.k[i], r.v[i]);
+  };
+  auto stage = [&](int st, const Raw& r) {
+#pragma unroll
+    for (int i = 0; i < PN; ++i) {
+      const int q = lt + 256 * i;
+      if (q >= MF_LOADERS) continue;  // a raw sub-block is at most MF_LOADERS pieces of 16 bytes
+      *reinterpret_cast<uint4*>(raw_buf(st, 0) + padded(16 * q)) = r.k[i];
+      *reinterpret_cast<uint4*>(raw_buf(st, 1) + padded(16 * q)) = r.v[i];
     }
-    compute(unit(i), i & 1, i == 0);
-    if (i == 0) DKV_TL(tl_mfma, 3);
+  };
+  if constexpr (SMALL) {
+    // One buffer: per unit, load, stage, dequantize and compute, with a barrier after the
+    // staging and one after the dequantization. The default plan gives each workgroup one unit;
+    // graph replays over longer histories may give it more, whose loads then wait for the unit
+    // before (no registers held across the MFMA work: four workgroups per CU need <= 128 VGPRs).
+    for (int i = 0; i < n; ++i) {
+      Raw r;
+      load(i, r);
+      if (i) __syncthreads();  // unit i - 1's MFMA work is done with the tiles
+      stage(0, r);
+      if (i == 0) DKV_TL(tl_mfma, 1);
+      __syncthreads();
+      dequant(unit(i), 0, 0);
+      if (i == 0) DKV_TL(tl_mfma, 2);
+      __syncthreads();
+      compute(unit(i), 0, i == 0);
+      if (i == 0) DKV_TL(tl_mfma, 3);
+    }
+  } else {
+    Raw r, r0, r2;
+    if (n > 0) load(0, r0);
+    if (n > 1) load(1, r);  // in flight while unit 0 is staged
+    // With two query blocks per wave (frame chunks, candidate batches) unit 2's loads go out at
+    // once too, not after unit 0 is staged and dequantized (past 1024 11.60 -> 11.37 us, 4096
+    // 13.98 -> 13.83). With one (decode steps), whose units compute little, the larger first
+    // burst delayed unit 0 more than it saved (11.68 -> 11.83 us at past 8128).
+    constexpr bool early2 = NBW == 2;
+    if (early2 && n > 2) load(2, r2);
+    if (n > 0) stage(0, r0);
+    // unit 0's load registers are settled on every path before the loop (the compiler does not
+    // tie the two n > 0 tests together and would otherwise wait on them inside the loop, where a
+    // wait also drains the prefetches in flight)
+    asm volatile("" ::"v"(r0.k[0].x), "v"(r0.k[0].y), "v"(r0.k[0].z), "v"(r0.k[0].w), "v"(r0.v[0].x),
+                 "v"(r0.v[0].y), "v"(r0.v[0].z), "v"(r0.v[0].w));
+    DKV_TL(tl_mfma, 1);
+    __syncthreads();
+    if (n > 0) dequant(unit(0), 0, 0);
+    DKV_TL(tl_mfma, 2);
+    if (n > 1) stage(1, r);
+    if (!early2 && n > 2) load(2, r);
+    for (int i = 0; i < n; ++i) {
+      __syncthreads();
+      if (i + 1 < n) dequant(unit(i + 1), (i + 1) & 1, (i + 1) & 1);
+      if (i + 2 < n) {
+        if (early2 && i == 0)
+          stage(0, r2);
+        else
+          stage(i & 1, r);
+        if (i + 3 < n) load(i + 3, r);
+      }
+      compute(unit(i), i & 1, i == 0);
+      if (i == 0) DKV_TL(tl_mfma, 3);
+    }
   }
   DKV_TL(tl_mfma, 4);
 
@@ -591,7 +645,7 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
   // groups fold and store at once); the other group parks its (max, sum, O)
   // for that block in LDS (over the staging buffers, once every wave is past
   // its last unit). Lane (g, col) of block nb holds O^T rows d = 16 db + 4 g + i
-  // of local row (w + KG_WAVES nb) * 16 + col.
+  // of local row (w + KGW nb) * 16 + col.
   auto owner = [](int nb) { return NBW == 2 ? nb : 0; };
   float lsum[NBW];
 #pragma unroll
@@ -599,13 +653,13 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
     lsum[nb] = group_sum(l_part[nb]);
   }
   float* mrg_o = reinterpret_cast<float*>(smem);
-  float2* mrg_ml = reinterpret_cast<float2*>(smem + MFMA_ROWS * MRG_STRIDE * 4);
+  float2* mrg_ml = reinterpret_cast<float2*>(smem + MROWS * MRG_STRIDE * 4);
   __syncthreads();
   if (wave_on) {
 #pragma unroll
     for (int nb = 0; nb < NBW; ++nb) {
       if (owner(nb) == kg) continue;  // this group finalizes the block; the other parks it
-      const int lr = (w + KG_WAVES * nb) * 16 + col;
+      const int lr = (w + KGW * nb) * 16 + col;
 #pragma unroll
       for (int db = 0; db < 4; ++db)
         *reinterpret_cast<f32x4*>(mrg_o + lr * MRG_STRIDE + 16 * db + 4 * g) = acc_o[nb][db];
@@ -618,7 +672,7 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
 #pragma unroll
     for (int nb = 0; nb < NBW; ++nb) {
       if (owner(nb) != kg) continue;
-      const int lr = (w + KG_WAVES * nb) * 16 + col;
+      const int lr = (w + KGW * nb) * 16 + col;
       const float2 o1 = mrg_ml[lr];
       const float mm = fmaxf(m_run[nb], o1.x);
       const float f0 = mm == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[nb] - mm);
@@ -704,7 +758,7 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
     }
     __syncthreads();
 #pragma unroll 1
-    for (int r = r0 + wave; r < r_end; r += MF_THREADS / 64)
+    for (int r = r0 + wave; r < r_end; r += 2 * KGW)
       merge_row_half<NBW == 1>(a, h, r, R, G, splits, active, part_o, part_ml);
     DKV_TL(tl_mfma, 9);
   }
@@ -725,19 +779,31 @@ static void launch_prec(const dkv_attn_args& a, const Plan& p, float* part_o, fl
   ArgTiles at;
   const NoArgTiles none = {0};
   const int rpg = p.rows_per_group;
-  if (fill_arg_tiles(a, at)) {
+  const bool argt = fill_arg_tiles(a, at);
+  if constexpr (PREC == 0) {
+    if (p.small) {  // decode steps: 4-wave workgroups, four per CU
+      if (argt)
+        hipLaunchKernelGGL((attn_mfma_kernel<PREC, 1, true, true>), grid, dim3(256), 0, s, at, a, p.units, p.splits,
+                           p.cap, rpg, part_o, part_ml DKV_MERGE_ARGS);
+      else
+        hipLaunchKernelGGL((attn_mfma_kernel<PREC, 1, false, true>), grid, dim3(256), 0, s, none, a, p.units,
+                           p.splits, p.cap, rpg, part_o, part_ml DKV_MERGE_ARGS);
+      return;
+    }
+  }
+  if (argt) {
     if (nbw >= 2)
-      hipLaunchKernelGGL((attn_mfma_kernel<PREC, 2, true>), grid, dim3(MF_THREADS), 0, s, at, a, p.units, p.splits,
-                         p.cap, rpg, part_o, part_ml DKV_MERGE_ARGS);
+      hipLaunchKernelGGL((attn_mfma_kernel<PREC, 2, true, false>), grid, dim3(MF_THREADS), 0, s, at, a, p.units,
+                         p.splits, p.cap, rpg, part_o, part_ml DKV_MERGE_ARGS);
     else
-      hipLaunchKernelGGL((attn_mfma_kernel<PREC, 1, true>), grid, dim3(MF_THREADS), 0, s, at, a, p.units, p.splits,
-                         p.cap, rpg, part_o, part_ml DKV_MERGE_ARGS);
+      hipLaunchKernelGGL((attn_mfma_kernel<PREC, 1, true, false>), grid, dim3(MF_THREADS), 0, s, at, a, p.units,
+                         p.splits, p.cap, rpg, part_o, part_ml DKV_MERGE_ARGS);
   } else if (nbw >= 2) {
-    hipLaunchKernelGGL((attn_mfma_kernel<PREC, 2, false>), grid, dim3(MF_THREADS), 0, s, none, a, p.units, p.splits,
-                       p.cap, rpg, part_o, part_ml DKV_MERGE_ARGS);
+    hipLaunchKernelGGL((attn_mfma_kernel<PREC, 2, false, false>), grid, dim3(MF_THREADS), 0, s, none, a, p.units,
+                       p.splits, p.cap, rpg, part_o, part_ml DKV_MERGE_ARGS);
   } else {
-    hipLaunchKernelGGL((attn_mfma_kernel<PREC, 1, false>), grid, dim3(MF_THREADS), 0, s, none, a, p.units, p.splits,
-                       p.cap, rpg, part_o, part_ml DKV_MERGE_ARGS);
+    hipLaunchKernelGGL((attn_mfma_kernel<PREC, 1, false, false>), grid, dim3(MF_THREADS), 0, s, none, a, p.units,
+                       p.splits, p.cap, rpg, part_o, part_ml DKV_MERGE_ARGS);
   }
 }
 

@@ -119,9 +119,11 @@ __device__ __forceinline__ void merge_row_f32(const dkv_attn_args& a, int h, int
 
 // Precision-0 merge (fp16 O / sum partials, 128 bytes per row in half_slot() order): one wave
 // per query row. Lane l = 8 j + c reads 16-byte chunk c and the (max, sum) of split s0 + 8 i + j
-// for i = 0..7, so each load instruction covers 8 splits, and accumulates 8 columns weighted by
-// that split's sum * 2^(m_s - M). Sums over j (lanes 8, 16 and 32 apart) finish the row, and
-// lanes 0..7 store it.
+// for i = 0..PER-1, so each load instruction covers 8 splits, and accumulates 8 columns weighted
+// by that split's sum * 2^(m_s - M). Sums over j (lanes 8, 16 and 32 apart) finish the row, and
+// lanes 0..7 store it. A pass reads 8 * PER splits with one round trip: 64 for frame chunks and
+// candidate batches, 128 for the plainly stored partials of decode steps (up to 128 splits per KV
+// head, which would otherwise take two dependent passes).
 template <bool PLAIN = false>
 __device__ __forceinline__ void merge_row_half(const dkv_attn_args& a, int h, int r, int R, int G, int splits,
                                                int active, const float* __restrict__ part_o,
@@ -134,29 +136,30 @@ __device__ __forceinline__ void merge_row_half(const dkv_attn_args& a, int h, in
   float M = -INFINITY, L = 0.f, acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-  for (int s0 = 0; s0 < active; s0 += 64) {
-    const int cnt = min(64, active - s0);
-    merge_f32x2 ml[8];
-    u32x4 raw[8];
+  constexpr int PER = PLAIN ? 16 : 8;
+  for (int s0 = 0; s0 < active; s0 += 8 * PER) {
+    const int cnt = min(8 * PER, active - s0);
+    merge_f32x2 ml[PER];
+    u32x4 raw[PER];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)  // splits past cnt load split cnt - 1 (no branches) and weigh 0
+    for (int i = 0; i < PER; ++i)  // splits past cnt load split cnt - 1 (no branches) and weigh 0
       ml[i] = merge_load<PLAIN>(mls + base + (int64_t)(s0 + min(8 * i + j, cnt - 1)) * R);
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < PER; ++i)
       raw[i] = merge_load<PLAIN>(rows + (base + (int64_t)(s0 + min(8 * i + j, cnt - 1)) * R) * 8 + c);
     __builtin_amdgcn_sched_barrier(0);  // every load issued before the first wait (one round trip)
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < PER; ++i)
       if (8 * i + j >= cnt) ml[i].x = -INFINITY;
     float bm = ml[0].x;
 #pragma unroll
-    for (int i = 1; i < 8; ++i) bm = fmaxf(bm, ml[i].x);
+    for (int i = 1; i < PER; ++i) bm = fmaxf(bm, ml[i].x);
     bm = fmaxf(bm, lane_xor8(bm));
     bm = fmaxf(max_over_hi(bm), M);
     // No branch on bm == -inf, as in merge_row_f32.
-    float w[8], lsum = 0.f;
+    float w[PER], lsum = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < PER; ++i) {
       const float f = ml[i].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml[i].x - bm);
       int ex;
       const float ls = half_partial_decode(ml[i].y, ex) * f;
@@ -170,7 +173,7 @@ __device__ __forceinline__ void merge_row_half(const dkv_attn_args& a, int h, in
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] *= f0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < PER; ++i) {
       const uint32_t q[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {

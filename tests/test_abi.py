@@ -204,7 +204,10 @@ def test_attend_workspace_matches_the_partial_format():
     """Per split row: 64 fp16 O / sum values + (max, sum) in bf16 precision, 64 fp32 O + (max, sum)
     in fp32 precision; the short-chunk kernel (path 3) keeps fp32 rows in both precisions, one
     split per 4 units (64-token tiles plus the chunk) by default, at most 64 per KV head. Auto
-    takes the frame-chunk kernel for decode steps too. One split needs no workspace."""
+    takes the frame-chunk kernel for decode steps too: in bf16 precision its 4-wave variant, four
+    workgroups per CU, so one unit per split up to that cap (4 x 256 CUs / 5 KV heads without a
+    device); in fp32 precision, and with path 2, the 12-wave kernel, one workgroup per CU. One
+    split needs no workspace."""
     lib = _lib.load()
     need = {}
     for precision in (0, 1):
@@ -222,7 +225,13 @@ def test_attend_workspace_matches_the_partial_format():
         assert lib.dkv_attend_workspace_bytes(ctypes.byref(one)) == 0
         auto = attn(past=4096, n_tiles=64, arena=4096, tiles=4096, nq=1, precision=precision)
         mfma = attn(past=4096, n_tiles=64, arena=4096, tiles=4096, nq=1, precision=precision, path=2)
-        assert lib.dkv_attend_workspace_bytes(ctypes.byref(auto)) == lib.dkv_attend_workspace_bytes(ctypes.byref(mfma))
+        units = 64 + 1
+        row = 64 * (4 if precision else 2) + 8  # fp32 O or fp16 O / sum, then (max, sum)
+        per = (units + 51 - 1) // 51  # 12 waves: one workgroup per CU, cap 256 // 5 = 51
+        big = mfma.heads * ((units + per - 1) // per) * 3 * row
+        assert lib.dkv_attend_workspace_bytes(ctypes.byref(mfma)) == big
+        # auto: bf16 one split per unit (65 <= 204), 3 query rows each; fp32 as path 2
+        assert lib.dkv_attend_workspace_bytes(ctypes.byref(auto)) == (auto.heads * units * 3 * row if precision == 0 else big)
 
 
 def test_pack_validate_checks_every_job_of_a_host_table():

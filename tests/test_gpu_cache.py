@@ -155,12 +155,13 @@ def test_graph_launches_keep_their_workspace(cuda):
 
 
 def test_graph_captured_first_survives_a_larger_capture_on_the_same_steps(cuda):
-    """Two graphs of 5-token steps captured on one GraphSteps: first on the frame-chunk kernel
-    (auto), then on the short-chunk kernel, whose fp32 partials (15 query rows per KV head, 64
-    workgroups per head for a launch sized by the cache's whole tile table: 1.27 MB) need a larger
-    workspace than begin_graph_steps() reserved (1 MiB). The steps hand the second capture a new
-    buffer but keep the first one, so replaying the first graph afterwards must still equal a
-    direct call on the same history, bit for bit."""
+    """Two graphs of 5-token steps captured on one GraphSteps: first on the 12-wave frame-chunk
+    kernel (path 'mfma', 51 splits' partials: 0.5 MB), then on the short-chunk kernel, whose fp32
+    partials (15 query rows per KV head, 64 workgroups per head for a launch sized by the cache's
+    whole tile table: 1.27 MB) need a larger workspace than the first capture's (1 MiB, the least
+    the steps allocate; begin_graph_steps() without q_heads reserves nothing ahead). The steps hand
+    the second capture a new buffer but keep the first one, so replaying the first graph
+    afterwards must still equal a direct call on the same history, bit for bit."""
     announce('cache: first graph survives a second capture that grows the steps workspace')
     g = torch.Generator().manual_seed(43)
     heads, q_heads = 5, 15
@@ -168,9 +169,9 @@ def test_graph_captured_first_survives_a_larger_capture_on_the_same_steps(cuda):
     q = torch.randn(1, q_heads, 5, 64, generator=g).to(torch.bfloat16).to(cuda)
     kn = torch.randn(1, heads, 5, 64, generator=g).to(torch.bfloat16).to(cuda)
     vn = torch.randn(1, heads, 5, 64, generator=g).to(torch.bfloat16).to(cuda)
-    steps = c.begin_graph_steps(5, q_heads=q_heads)
+    steps = c.begin_graph_steps(5)
     graphs, outs, sizes = [], [], []
-    for path in ('auto', 'short'):
+    for path in ('mfma', 'short'):
         c.reset()
         c.begin_graph_steps(5, steps=steps)
         c.select(16)
@@ -194,7 +195,7 @@ def test_graph_captured_first_survives_a_larger_capture_on_the_same_steps(cuda):
         c.append(torch.randn(1, heads, 64, 64, generator=g).to(torch.bfloat16).to(cuda),
                  torch.randn(1, heads, 64, 64, generator=g).to(torch.bfloat16).to(cuda), 0)
     past = c.seen[0]
-    for path, graph, out in zip(('auto', 'short'), graphs, outs):
+    for path, graph, out in zip(('mfma', 'short'), graphs, outs):
         f = c.fork()  # same arena and tile table: the steps re-attach to it
         f.begin_graph_steps(5, steps=steps)
         f.select(16)
