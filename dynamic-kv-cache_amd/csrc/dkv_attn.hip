@@ -287,6 +287,47 @@ combine_half_kernel(dkv_attn_args a, int splits, int cap, int short_plan, const 
   DKV_TL(tl_comb, 3);
 }
 
+// The same merges with MERGE_WAVES waves per query row (one row per workgroup, merge_row_*_wide):
+// each wave merges a contiguous share of the splits and wave 0 combines the shares in wave order.
+// A wave of the one-row-per-wave kernels above is alone on its SIMD, so every dependent load wait
+// and instruction of its merge is on the critical path; a share of a quarter of the splits takes a
+// quarter of that.
+template <bool PLAIN>
+__global__ void __launch_bounds__(64 * MERGE_WAVES)
+combine_wide_kernel(dkv_attn_args a, int splits, int cap, const float* __restrict__ part_o,
+                    const float2* __restrict__ part_ml) {
+  DKV_TL(tl_comb, 0);
+  const int h = blockIdx.y, r = blockIdx.x;
+  const int G = a.q_heads / a.heads;
+  const int R = G * a.nq;
+  if (r >= R) return;  // uniform over the workgroup
+  int units = a.n_tiles + (a.nq + TILE - 1) / TILE;
+  Hist hs;
+  const int active = runtime_plan(a, hs, units, splits, cap);
+  if (active <= 1) return;
+  DKV_TL(tl_comb, 1);
+  merge_row_f32_wide<PLAIN, MERGE_WAVES>(a, h, r, R, G, splits, active, part_o, part_ml);
+  DKV_TL(tl_comb, 3);
+}
+
+template <bool PLAIN>
+__global__ void __launch_bounds__(64 * MERGE_WAVES)
+combine_half_wide_kernel(dkv_attn_args a, int splits, int cap, const float* __restrict__ part_o,
+                         const float2* __restrict__ part_ml) {
+  DKV_TL(tl_comb, 0);
+  const int h = blockIdx.y, r = blockIdx.x;
+  const int G = a.q_heads / a.heads;
+  const int R = G * a.nq;
+  if (r >= R) return;  // uniform over the workgroup
+  int units = a.n_tiles + (a.nq + TILE - 1) / TILE;
+  Hist hs;
+  const int active = runtime_plan(a, hs, units, splits, cap);
+  if (active <= 1) return;
+  DKV_TL(tl_comb, 1);
+  merge_row_half_wide<PLAIN, MERGE_WAVES>(a, h, r, R, G, splits, active, part_o, part_ml);
+  DKV_TL(tl_comb, 3);
+}
+
 // ---------------------------------------------------------------------------
 // Host side.
 
@@ -428,6 +469,11 @@ static Plan make_plan(const dkv_attn_args& a) {
     }
   }
   p.plain_parts = p.path == 2 && splits > 1 && mfma_blocks_per_wave(p.rows_per_group) == 1;
+  // The merge with MERGE_WAVES waves per row where the one-wave merge would leave most SIMDs idle
+  // (decode steps: 3-12 rows per KV head, 43-128 splits; 9.78 -> 9.11 us per layer at past 8128,
+  // 4 tokens 10.52 -> 9.52). With more rows the one-wave merge already has a wave on most SIMDs,
+  // and four times the workgroups ran slower (frame chunks at past 8128 15.80 -> 17.28 us).
+  p.wide_merge = MERGE_WAVES > 1 && p.path != 3 && (int64_t)a.heads * R * MERGE_WAVES <= 4 * num_cus();
   p.fused = DKV_INKERNEL_MERGE && a.path == 0 && p.path == 2 && p.precision == 0 && splits > 1 &&
             a.heads * p.row_groups * 4 <= INKERNEL_COUNTER_BYTES;
   if (splits > 1) {
@@ -475,7 +521,21 @@ static int launch_attend(const dkv_attn_args& a, const Plan& p, void* ws, hipStr
     const int R = (a.q_heads / a.heads) * a.nq;
     const int short_plan = p.path == 3;
     const dim3 grid((R + 3) / 4, a.heads);
-    if (p.precision == 1 || short_plan) {  // the short-chunk kernel's partials are fp32 in both precisions
+    if (p.wide_merge) {
+      const dim3 wgrid(R, a.heads);
+      if (p.precision == 1) {
+        if (p.plain_parts)
+          hipLaunchKernelGGL(combine_wide_kernel<true>, wgrid, dim3(64 * MERGE_WAVES), 0, s, a, p.splits, p.cap, part_o, part_ml);
+        else
+          hipLaunchKernelGGL(combine_wide_kernel<false>, wgrid, dim3(64 * MERGE_WAVES), 0, s, a, p.splits, p.cap, part_o, part_ml);
+      } else if (p.plain_parts) {
+        hipLaunchKernelGGL(combine_half_wide_kernel<true>, wgrid, dim3(64 * MERGE_WAVES), 0, s, a, p.splits, p.cap,
+                           part_o, part_ml);
+      } else {
+        hipLaunchKernelGGL(combine_half_wide_kernel<false>, wgrid, dim3(64 * MERGE_WAVES), 0, s, a, p.splits, p.cap,
+                           part_o, part_ml);
+      }
+    } else if (p.precision == 1 || short_plan) {  // the short-chunk kernel's partials are fp32 in both precisions
       if (p.plain_parts)
         hipLaunchKernelGGL(combine_kernel<true>, grid, dim3(256), 0, s, a, p.splits, p.cap, short_plan, part_o, part_ml);
       else

@@ -207,6 +207,7 @@ struct Plan {
   int fused;      // the in-kernel merge build: the frame-chunk kernel merges its own splits
   int plain_parts;  // MFMA split partials of the one-block-per-wave variant: plain stores and loads
   int small;      // MFMA decode-step variant: 4-wave workgroups, four per CU (MFMA_SMALL_ROWS)
+  int wide_merge; // split merge with MERGE_WAVES waves per query row (combine_wide_*_kernel)
   int64_t part_o_bytes, part_ml_bytes;
 };
 
@@ -254,6 +255,13 @@ constexpr int MFMA_SMALL_ROWS = 32;
 // per CU, and two units per workgroup ran slower than the 12-wave kernel (12.24 vs 11.24 us for
 // a decode step at past 8128), so only precision 0 takes this variant.
 constexpr int MFMA_SMALL_PER_CU = 4;
+
+// Waves per query row of the split merge (combine_wide_kernel, combine_half_wide_kernel); 1 keeps
+// the one-wave-per-row merge kernels (a build option for comparisons).
+#ifndef DKV_MERGE_WAVES
+#define DKV_MERGE_WAVES 4
+#endif
+constexpr int MERGE_WAVES = DKV_MERGE_WAVES;
 
 // Precision-0 split partials hold O / sum in fp16, 64 values per row (128
 // bytes) in the order the MFMA kernel's lanes store them: the lane of 16-byte

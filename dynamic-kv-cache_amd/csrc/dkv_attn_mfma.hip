@@ -51,8 +51,10 @@
 // partial stores (vmcnt 0) and counts its arrival on its (KV head, row
 // group)'s counter with an agent-scope release; the workgroup that arrives
 // last acquires, resets the counter for the next launch and merges every split
-// with the merge kernel's row arithmetic (dkv_merge.h), so the output bits
-// equal the two-launch path's. No workgroup waits for another. Timed on this
+// with the one-wave merge's row arithmetic (dkv_merge.h), so the output bits
+// equal the two-launch path's wherever that merges one row per wave (launches
+// of few rows use the wide merge, which sums in another order). No workgroup
+// waits for another. Timed on this
 // kernel, the arrival comes 2-3 us after a workgroup's stores, and one
 // workgroup then reads all of its KV head's partials: decode steps at past
 // 8128 ran 13.8 us against 11.7 with the second launch, and a 64-token frame
