@@ -285,6 +285,38 @@ def test_more_splits_than_one_merge_pass(cuda, precision, path):
         assert err <= max(2e-2, noise), (err, noise)
 
 
+@pytest.mark.parametrize('precision', ['fp32', 'bf16'])
+@pytest.mark.parametrize('nq', [1, 4])
+def test_decode_step_merges_with_four_waves_per_row(cuda, nq, precision):
+    """Decode steps merge their splits with four waves per query row, each wave over a quarter of
+    the splits (2, 3 and 5 splits leave some waves none; 128 = one per unit at past 8128 needs one
+    pass per wave). Every count stays within the bounds of the single-split results, and a repeat
+    of the same call gives the same bits (the four shares are combined in wave order)."""
+    announce(f'attention decode four-wave merge nq={nq} precision={precision}')
+    case = frame_chunk_case(8128, seed=61 + nq, nq=nq)
+    c, dk, dv = build(case, cuda)
+    if precision == 'fp32':
+        ref, tol = oracle_out(case, dk, dv), 1e-3
+    else:
+        ref = semantics_out(case, dk, dv, None, torch.float32)
+        tol = max(2e-2, reference_noise(case, dk, dv))
+    q, kn, vn = (case[x][None].to(cuda) for x in ('q', 'k_new', 'v_new'))
+    c.select(16)
+    past = c.append(kn, vn, 0)
+
+    def attend(splits):
+        out = c.attend(q, kn, vn, 0, past, out_dtype=torch.float32, splits=splits, precision=precision)
+        torch.cuda.synchronize()
+        return out[0].cpu().double()
+
+    for splits in (2, 3, 5, 1000, 0):
+        got = attend(splits)
+        err = (got - ref).abs().max().item()
+        print(f'[decode merge] nq={nq} {precision} splits={splits}: max-abs {err:.4e} (bound {tol:.4e})', flush=True)
+        assert err <= tol, (splits, err, tol)
+        assert torch.equal(got, attend(splits)), splits
+
+
 @pytest.mark.parametrize('path', PATHS)
 @pytest.mark.parametrize('splits', [0, 1000])
 def test_bf16_split_partials_keep_large_values_finite(cuda, splits, path):
