@@ -402,23 +402,27 @@ rope_pack_kernel(const uint16_t* __restrict__ qkv, int64_t qkv_stride, const uin
   const int t = valid ? tok : n - 1;  // rows past the end read the last row and store nothing
   const bool is_v = hh >= q_heads + heads;
 
-  u32x4 w = *reinterpret_cast<const u32x4*>(qkv + (int64_t)t * qkv_stride + hh * D + 8 * c);
-  if (!is_v) {
-    const int64_t o = (int64_t)t * cs_stride + 8 * c;
-    const u32x4 cs = *reinterpret_cast<const u32x4*>(cosv + o);
-    const u32x4 sn = *reinterpret_cast<const u32x4*>(sinv + o);
-    // rotate_half pairs column d with d +- 32: lane c with lane c ^ 4 of the same row
-    u32x4 p;
+  // Every load first, so that they form one round trip: the row, its cos and sin, and the pack job
+  // (scalar loads). Placed by their uses (the rotation of Q and K rows, the pack of K and V rows),
+  // they went out after the row had arrived: two more round trips. V rows are rotated too and
+  // keep their input (a select, not a branch the loads could be moved into).
+  const dkv_pack_job j = DEVJOB ? *djob : hjob;
+  const u32x4 x = *reinterpret_cast<const u32x4*>(qkv + (int64_t)t * qkv_stride + hh * D + 8 * c);
+  const int64_t o = (int64_t)t * cs_stride + 8 * c;
+  const u32x4 cs = *reinterpret_cast<const u32x4*>(cosv + o);
+  const u32x4 sn = *reinterpret_cast<const u32x4*>(sinv + o);
+  asm volatile("" ::: "memory");  // the job's loads stay above it
+  // rotate_half pairs column d with d +- 32: lane c with lane c ^ 4 of the same row
+  u32x4 p;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) p[e] = __shfl_xor(w[e], 4);
-    w = rope8(w, p, cs, sn, c < 4);
-  }
+  for (int e = 0; e < 4; ++e) p[e] = __shfl_xor(x[e], 4);
+  const u32x4 rot = rope8(x, p, cs, sn, c < 4);
+  const u32x4 w = is_v ? x : rot;
   uint16_t* dst = hh < q_heads ? q_out + (int64_t)hh * n * D
                                : (is_v ? v_out + (int64_t)(hh - q_heads - heads) * n * D
                                        : k_out + (int64_t)(hh - q_heads) * n * D);
   if (valid) *reinterpret_cast<u32x4*>(dst + (int64_t)tok * D + 8 * c) = w;
 
-  const dkv_pack_job j = DEVJOB ? *djob : hjob;
   if (gw == 0 && j.write_tiles) write_segment_tiles(j, layers, heads, tiles);
   if (hh < q_heads) return;
   const bool packs = valid && tok < j.n;  // rows the job packs
