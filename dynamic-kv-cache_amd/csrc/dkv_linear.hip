@@ -90,6 +90,20 @@ __global__ void __launch_bounds__(64 * WAVES) linear_kernel(const LinearArgs a) 
     xrow[rb] = a.x + (int64_t)row * a.ldx + 8 * g;
   }
 
+  constexpr int TILES = RB * NB, OUT = RB * NT;
+  // The residual of the output tiles this wave finishes (tile o belongs to wave o % WAVES), loaded
+  // first, so that it arrives with the operands: loaded in the epilogue it was one more memory
+  // round trip after the reduction. Rows past the end read the last row (never stored).
+  uint2 resv[EPI == EPI_RESIDUAL ? OUT : 1];
+  if constexpr (EPI == EPI_RESIDUAL) {
+#pragma unroll
+    for (int o = 0; o < OUT; ++o) {
+      if (o % WAVES != wave) continue;
+      const int row = min((rg * RB + o / NT) * 16 + col, a.rows - 1);
+      resv[o] = *reinterpret_cast<const uint2*>(a.res + (int64_t)row * a.ldr + n0 + 16 * (o % NT) + 4 * g);
+    }
+  }
+
   // Every load of this wave's pairs (the host guarantees CH * WAVES >= kp) is
   // issued before the first MFMA. With the RMSNorm prologue the x rows and
   // the norm weight go first, unconditionally (a pair past kp loads pair
@@ -199,7 +213,6 @@ __global__ void __launch_bounds__(64 * WAVES) linear_kernel(const LinearArgs a) 
   // phase (at most 32 KB of partials). Output tile o = (rb, nt) belongs to
   // wave o % WAVES, which sums its gate (and up) partial tiles and runs the
   // epilogue.
-  constexpr int TILES = RB * NB, OUT = RB * NT;
   constexpr int TP = TILES < 32 / WAVES ? TILES : 32 / WAVES;
   __shared__ f32x4_t red[WAVES][TP][64];
   f32x4_t gsum[OUT], usum[OUT];
@@ -243,7 +256,7 @@ __global__ void __launch_bounds__(64 * WAVES) linear_kernel(const LinearArgs a) 
 #pragma unroll
     for (int e = 0; e < 4; ++e) y[e] = round_bf16(gsum[o][e]);
     if (EPI == EPI_RESIDUAL) {
-      const uint2 r = *reinterpret_cast<const uint2*>(a.res + (int64_t)row * a.ldr + c);
+      const uint2 r = resv[o];
       y[0] += bf16_lo(r.x);
       y[1] += bf16_hi(r.x);
       y[2] += bf16_lo(r.y);
