@@ -245,6 +245,16 @@ attn_vec_kernel(dkv_attn_args a, int units, int splits, int cap, float* __restri
 static __device__ uint64_t tl_comb[TL_SLOTS * TL_EVENTS];
 #endif
 //
+// The arguments the merge kernels read before their first partial load, read together: placed by
+// their uses, the compiler issued these scalar loads in four to six dependent rounds (each a
+// round trip to the cache hierarchy); the empty asm needs them all at once.
+__device__ __forceinline__ void merge_args_at_once(const dkv_attn_args& a, int splits, int cap, const void* part_o,
+                                                   const void* part_ml) {
+  asm volatile("" ::"s"(a.q_heads), "s"(a.heads), "s"(a.nq), "s"(a.n_tiles), "s"(a.past), "s"(a.step), "s"(splits),
+               "s"(cap), "s"(part_o), "s"(part_ml), "s"(a.out), "s"(a.out_tok_stride), "s"(a.out_head_stride),
+               "s"(a.out_dtype));
+}
+
 // The two merge kernels: one wave per query row of a KV head, the row's arithmetic in
 // merge_row_f32 (precision 1) and merge_row_half (precision 0), dkv_merge.h.
 template <bool PLAIN>
@@ -252,6 +262,7 @@ __global__ void __launch_bounds__(256)
 combine_kernel(dkv_attn_args a, int splits, int cap, int short_plan, const float* __restrict__ part_o,
                const float2* __restrict__ part_ml) {
   DKV_TL(tl_comb, 0);
+  merge_args_at_once(a, splits, cap, part_o, part_ml);
   const int h = blockIdx.y;
   const int G = a.q_heads / a.heads;
   const int R = G * a.nq;
@@ -272,6 +283,7 @@ __global__ void __launch_bounds__(256)
 combine_half_kernel(dkv_attn_args a, int splits, int cap, int short_plan, const float* __restrict__ part_o,
                     const float2* __restrict__ part_ml) {
   DKV_TL(tl_comb, 0);
+  merge_args_at_once(a, splits, cap, part_o, part_ml);
   const int h = blockIdx.y;
   const int G = a.q_heads / a.heads;
   const int R = G * a.nq;
@@ -297,6 +309,7 @@ __global__ void __launch_bounds__(64 * MERGE_WAVES)
 combine_wide_kernel(dkv_attn_args a, int splits, int cap, const float* __restrict__ part_o,
                     const float2* __restrict__ part_ml) {
   DKV_TL(tl_comb, 0);
+  merge_args_at_once(a, splits, cap, part_o, part_ml);
   const int h = blockIdx.y, r = blockIdx.x;
   const int G = a.q_heads / a.heads;
   const int R = G * a.nq;
@@ -315,6 +328,7 @@ __global__ void __launch_bounds__(64 * MERGE_WAVES)
 combine_half_wide_kernel(dkv_attn_args a, int splits, int cap, const float* __restrict__ part_o,
                          const float2* __restrict__ part_ml) {
   DKV_TL(tl_comb, 0);
+  merge_args_at_once(a, splits, cap, part_o, part_ml);
   const int h = blockIdx.y, r = blockIdx.x;
   const int G = a.q_heads / a.heads;
   const int R = G * a.nq;

@@ -297,6 +297,18 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
   };
 
   DKV_TL(tl_mfma, 0);
+  // Every argument that the first history and query loads depend on, read together: placed by
+  // their uses, the compiler issued these scalar loads in seven dependent rounds (each a round
+  // trip to the cache hierarchy) before the first history load; the empty asm needs them all at
+  // once, so they go out in one round.
+  if constexpr (ARGT)
+    asm volatile("" ::"s"(units), "s"(splits), "s"(cap), "s"(rpg), "s"(a.past), "s"(a.n_tiles), "s"(a.step),
+                 "s"(a.heads), "s"(a.q_heads), "s"(a.nq), "s"(a.q), "s"(a.q_head_stride), "s"(a.q_tok_stride),
+                 "s"(a.arena), "s"(a.layer), "s"(a.n_segs), "s"(a.scale));
+  else
+    asm volatile("" ::"s"(units), "s"(splits), "s"(cap), "s"(rpg), "s"(a.past), "s"(a.n_tiles), "s"(a.step),
+                 "s"(a.heads), "s"(a.q_heads), "s"(a.nq), "s"(a.q), "s"(a.q_head_stride), "s"(a.q_tok_stride),
+                 "s"(a.arena), "s"(a.layer), "s"(a.n_segs), "s"(a.scale), "s"(a.tiles));
   Hist hs;
   const int active = runtime_plan(a, hs, units, splits, cap);
   const int split = blockIdx.x, h = blockIdx.y, rg = blockIdx.z;
