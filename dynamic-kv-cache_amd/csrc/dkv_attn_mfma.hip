@@ -301,10 +301,16 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
   // their uses, the compiler issued these scalar loads in seven dependent rounds (each a round
   // trip to the cache hierarchy) before the first history load; the empty asm needs them all at
   // once, so they go out in one round.
+  // A decode launch of the default plan has as many splits as units, so workgroup s walks unit s
+  // alone: with the descriptors in the argument block, descriptor s is read in the same round and
+  // used when u0 == s turns out to hold (a guess that costs one scalar load when it does not).
+  uint4 spec = make_uint4(0, 0, 0, 0);
+  if constexpr (ARGT && SMALL) spec = arg_tile(min((int)blockIdx.x, DKV_ARG_TILES - 1));
   if constexpr (ARGT)
     asm volatile("" ::"s"(units), "s"(splits), "s"(cap), "s"(rpg), "s"(a.past), "s"(a.n_tiles), "s"(a.step),
                  "s"(a.heads), "s"(a.q_heads), "s"(a.nq), "s"(a.q), "s"(a.q_head_stride), "s"(a.q_tok_stride),
-                 "s"(a.arena), "s"(a.layer), "s"(a.n_segs), "s"(a.scale));
+                 "s"(a.arena), "s"(a.layer), "s"(a.n_segs), "s"(a.scale), "s"(spec.x), "s"(spec.y), "s"(spec.z),
+                 "s"(spec.w));
   else
     asm volatile("" ::"s"(units), "s"(splits), "s"(cap), "s"(rpg), "s"(a.past), "s"(a.n_tiles), "s"(a.step),
                  "s"(a.heads), "s"(a.q_heads), "s"(a.nq), "s"(a.q), "s"(a.q_head_stride), "s"(a.q_tok_stride),
@@ -580,7 +586,11 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
   // Wait for the window here, on every path (unit 0 reads it next anyway): a wait the compiler
   // cannot place before the loop lands inside it, where it also waits for the prefetches in flight.
   asm volatile("" ::"v"(win.x), "v"(win.y), "v"(win.z), "v"(win.w));
-  auto unit = [&](int rel) { return unit_at(a, hs, u0 + rel, rel, h, win, in_args); };
+  auto unit = [&](int rel) {
+    if (ARGT && SMALL && rel == 0 && u0 == split && u0 < hs.n_tiles)  // wave-uniform
+      return history_unit(a, hs, spec.x, spec.y, spec.z, spec.w, h);
+    return unit_at(a, hs, u0 + rel, rel, h, win, in_args);
+  };
   // A thread's raw bytes of one unit: PN pieces of K and of V.
   struct Raw {
     uint4 k[PN], v[PN];
