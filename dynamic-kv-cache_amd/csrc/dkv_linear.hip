@@ -66,6 +66,12 @@ __device__ __forceinline__ float lane_group_sum(float x) {
 template <int CH, int NT, int WAVES, int RB, int EPI, bool NORM>
 __global__ void __launch_bounds__(64 * WAVES) linear_kernel(const LinearArgs a) {
   constexpr int NB = EPI == EPI_SILU_MUL ? 2 * NT : NT;  // column blocks multiplied
+  // The arguments the first loads depend on, read together (placed by their uses, the compiler
+  // read them in two dependent rounds of scalar loads, each a round trip to the cache hierarchy).
+  asm volatile("" ::"s"(a.x), "s"(a.ldx), "s"(a.w), "s"(a.ldw), "s"(a.rows), "s"(a.kp), "s"(a.n_tiles),
+               "s"(a.row_groups), "s"(a.up));
+  if constexpr (NORM) asm volatile("" ::"s"(a.norm));
+  if constexpr (EPI == EPI_RESIDUAL) asm volatile("" ::"s"(a.res), "s"(a.ldr));
   const int b = blockIdx.x;
   const int xcd = b & 7, j = b >> 3;
   const int rg = j % a.row_groups;
