@@ -209,22 +209,34 @@ __device__ __forceinline__ int loader_index(int wave, int lane) {
 
 // One 16-byte piece of K (loader index p = 0..511 -> pieces 0..511) and one of V;
 // threads with p >= 512 load nothing (every sub-block is at most 512 pieces).
+// Lanes whose piece is past the unit's bytes (or past the chunk's rows) load nothing and keep the
+// registers' previous contents, which the staging copies to LDS bytes that dequantization never
+// reads. Writing zeros into them here (the first version did) made the compiler wait for every
+// load in flight before each unit's loads, since another branch's loads into the same registers
+// could have been pending: units 1 and 2, prefetched at kernel start, went out only after unit
+// 0's (and then unit 1's) bytes had arrived. The callers zero the registers once, before any load.
 __device__ __forceinline__ void raw_load(const dkv_attn_args& a, const Unit& un, int h, int p, uint4& wk, uint4& wv) {
-  wk = wv = make_uint4(0, 0, 0, 0);
+  // The kind of unit picks the addresses; one pair of loads after the choice (with a pair in each
+  // branch, the registers' values had to be merged after the loads, and the copies waited for them).
+  const uint8_t* kp;
+  const uint8_t* vp;
+  bool ok;
   if (un.chunk) {
     const int row = p >> 3, c = p & 7;
-    if (row < un.valid) {
-      const int64_t j = un.first + row;
-      wk = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.k_new) + h * a.kn_head_stride +
-                                           j * a.kn_tok_stride + c * 8);
-      wv = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.v_new) + h * a.vn_head_stride +
-                                           j * a.vn_tok_stride + c * 8);
-    }
-  } else if (p < (int)(subblock_bytes(un.rows, un.bits) >> 4)) {
-    // history bytes are read once per launch: nontemporal loads (past 8128: 19.0 -> 18.6 us per
-    // layer, a decode step 13.6 -> 13.0 us)
-    wk = __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(un.ksub) + p));
-    wv = __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(un.vsub) + p));
+    ok = row < un.valid;
+    const int64_t j = un.first + row;
+    kp = static_cast<const uint8_t*>(a.k_new) + 2 * (h * a.kn_head_stride + j * a.kn_tok_stride + c * 8);
+    vp = static_cast<const uint8_t*>(a.v_new) + 2 * (h * a.vn_head_stride + j * a.vn_tok_stride + c * 8);
+  } else {
+    ok = p < (int)(subblock_bytes(un.rows, un.bits) >> 4);
+    kp = un.ksub + 16 * p;
+    vp = un.vsub + 16 * p;
+  }
+  // history bytes are read once per launch: nontemporal loads (past 8128: 19.0 -> 18.6 us per
+  // layer, a decode step 13.6 -> 13.0 us); the chunk's rows are read by one workgroup each too
+  if (ok) {
+    wk = __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp)));
+    wv = __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vp)));
   }
 }
 
@@ -599,6 +611,15 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
 #pragma unroll
     for (int i = 0; i < PN; ++i) raw_load(a, unit(rel), h, lt + 256 * i, r.k[i], r.v[i]);
   };
+  // The zeros of a Raw, made opaque where they are written (the kernel's start): the compiler
+  // would otherwise move them down to the loads, and each move brings back the wait described at
+  // raw_load.
+  auto opaque = [&](Raw& r) {
+#pragma unroll
+    for (int i = 0; i < PN; ++i)
+      asm volatile("" : "+v"(r.k[i].x), "+v"(r.k[i].y), "+v"(r.k[i].z), "+v"(r.k[i].w), "+v"(r.v[i].x),
+                   "+v"(r.v[i].y), "+v"(r.v[i].z), "+v"(r.v[i].w));
+  };
   auto stage = [&](int st, const Raw& r) {
 #pragma unroll
     for (int i = 0; i < PN; ++i) {
@@ -613,8 +634,9 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
     // staging and one after the dequantization. The default plan gives each workgroup one unit;
     // graph replays over longer histories may give it more, whose loads then wait for the unit
     // before (no registers held across the MFMA work: four workgroups per CU need <= 128 VGPRs).
+    Raw r = {};
+    opaque(r);
     for (int i = 0; i < n; ++i) {
-      Raw r;
       load(i, r);
       if (i) __syncthreads();  // unit i - 1's MFMA work is done with the tiles
       stage(0, r);
@@ -627,7 +649,10 @@ attn_mfma_kernel(typename std::conditional<ARGT, ArgTiles, NoArgTiles>::type, dk
       if (i == 0) DKV_TL(tl_mfma, 3);
     }
   } else {
-    Raw r, r0, r2;
+    Raw r = {}, r0 = {}, r2 = {};
+    opaque(r);
+    opaque(r0);
+    opaque(r2);
     if (n > 0) load(0, r0);
     if (n > 1) load(1, r);  // in flight while unit 0 is staged
     // With two query blocks per wave (frame chunks, candidate batches) unit 2's loads go out at
