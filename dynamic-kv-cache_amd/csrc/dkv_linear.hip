@@ -114,11 +114,23 @@ __global__ void __launch_bounds__(64 * WAVES) linear_kernel(const LinearArgs a) 
   // issued before the first MFMA. With the RMSNorm prologue the x rows and
   // the norm weight go first, unconditionally (a pair past kp loads pair
   // kp - 1 and is skipped below, so the loads form one straight-line block
-  // whose uses wait for exactly what they need): the prologue waits only for
-  // them and normalizes while the weight tiles, which come from HBM, are in
-  // flight. Without it the first MFMA needs both, and pairs past kp (p < kp is
-  // uniform over the wave) load nothing.
+  // whose uses wait for exactly what they need), and the weight tiles, which
+  // come from HBM, only once x has arrived (load_weights below): the prologue
+  // normalizes while they are in flight. Without it the first MFMA needs both,
+  // and pairs past kp (p < kp is uniform over the wave) load nothing.
   Op8 xa[CH][2][RB], wa[CH][2][NB], gn[NORM ? CH : 1][2];
+  auto load_weights = [&]() {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int p = min(wave + WAVES * i, a.kp - 1);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int k = 64 * p + 32 * h;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) wa[i][h][nb].u = *reinterpret_cast<const u32x4*>(wrow[nb] + k);
+      }
+    }
+  };
   if constexpr (NORM) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
@@ -129,24 +141,6 @@ __global__ void __launch_bounds__(64 * WAVES) linear_kernel(const LinearArgs a) 
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) xa[i][h][rb].u = *reinterpret_cast<const u32x4*>(xrow[rb] + k);
         gn[i][h].u = *reinterpret_cast<const u32x4*>(a.norm + k + 8 * g);
-      }
-    }
-    // Every wave's x and norm loads reach the memory pipeline before any wave's weight loads: the
-    // CU takes the waves' loads in the order they are issued, and without this barrier the later
-    // waves' x rows queued behind the first waves' weight tiles, which come from HBM, so the
-    // normalization barrier waited ~1-2 us longer for them (Q/K/V 6.32 -> 5.24 us, gate/up 10.66 -> 10.12 us per
-    // launch in a chain of 32 dependent launches). The barrier waits for no memory.
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const int p = min(wave + WAVES * i, a.kp - 1);
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int k = 64 * p + 32 * h;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) wa[i][h][nb].u = *reinterpret_cast<const u32x4*>(wrow[nb] + k);
       }
     }
   } else {
@@ -165,7 +159,7 @@ __global__ void __launch_bounds__(64 * WAVES) linear_kernel(const LinearArgs a) 
       }
     }
   }
-  if (NORM) {
+  if constexpr (NORM) {
     __shared__ float ssum[WAVES][RB][16];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
@@ -185,7 +179,17 @@ __global__ void __launch_bounds__(64 * WAVES) linear_kernel(const LinearArgs a) 
       ss = lane_group_sum(ss);
       if (g == 0) ssum[wave][rb][col] = ss;
     }
+    // The weight tiles go out once x is in: issued with x, the CU took the waves' loads in issue
+    // order and the later waves' x rows queued behind the first waves' weight tiles, so the
+    // normalization barrier waited 1-2 us longer for them. A wave issues its weights when its own
+    // x has arrived, or, with 32 x rows per workgroup (the SiLU*up shape), when every wave's has
+    // (after the barrier): in a chain of 32 dependent launches Q/K/V took 6.32 us per launch with
+    // the weights issued with x, 5.24 with them after a barrier that waits for no memory, 5.13
+    // after the wave's own x, 5.44 after every wave's; gate/up 10.66, 10.12, 9.85 and 9.70 us.
+    constexpr bool AFTER_BARRIER = RB > 1;
+    if constexpr (!AFTER_BARRIER) load_weights();
     __syncthreads();
+    if constexpr (AFTER_BARRIER) load_weights();
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       float tot = 0.f;
