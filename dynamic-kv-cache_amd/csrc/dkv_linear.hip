@@ -52,8 +52,16 @@ struct LinearArgs {  // passed by value and never written (a written copy would 
   int rows, k, kp;  // kp = k / 64
   int n_tiles;      // column tiles of 16 * NT output columns
   int row_groups;   // ceil(rows / (16 * RB))
-  int up;           // EPI_SILU_MUL: first weight row of the up half (= inter)
+  int up;           // n_out (EPI_SILU_MUL: the first weight row of the up half)
+  int layout;       // LAYOUT_* bits: which of w, x and out are MFMA-tiled
 };
+
+// Operand layouts. Rows of k contiguous elements, or MFMA-tiled: the 16 rows x 64 k of one pair
+// of MFMA steps are 2 KB in the order the lanes read them, one 1 KB half per step (element (r, c)
+// at ((r / 16) * kp + c / 64) * 1024 + (c / 32 % 2) * 512 + ((c / 8 % 4) * 16 + r % 16) * 8 + c % 8),
+// so that each 16-byte-per-lane load instruction reads 1 KB of consecutive bytes (8 full cache
+// lines instead of 64-byte halves of 16). A tiled x or out has its rows rounded up to 16.
+enum { LAYOUT_W_TILED = DKV_LINEAR_W_TILED, LAYOUT_X_TILED = DKV_LINEAR_X_TILED, LAYOUT_OUT_TILED = DKV_LINEAR_OUT_TILED };
 
 __device__ __forceinline__ float lane_group_sum(float x) {
   // sum over lanes col, col + 16, col + 32, col + 48 (gfx950 lane swaps)
@@ -63,13 +71,13 @@ __device__ __forceinline__ float lane_group_sum(float x) {
   return __uint_as_float(q[0]) + __uint_as_float(q[1]);
 }
 
-template <int CH, int NT, int WAVES, int RB, int EPI, bool NORM>
+template <int CH, int NT, int WAVES, int RB, int EPI, bool NORM, int OPS>
 __global__ void __launch_bounds__(64 * WAVES) linear_kernel(const LinearArgs a) {
   constexpr int NB = EPI == EPI_SILU_MUL ? 2 * NT : NT;  // column blocks multiplied
   // The arguments the first loads depend on, read together (placed by their uses, the compiler
   // read them in two dependent rounds of scalar loads, each a round trip to the cache hierarchy).
   asm volatile("" ::"s"(a.x), "s"(a.ldx), "s"(a.w), "s"(a.ldw), "s"(a.rows), "s"(a.kp), "s"(a.n_tiles),
-               "s"(a.row_groups), "s"(a.up));
+               "s"(a.row_groups), "s"(a.up), "s"(a.layout));
   if constexpr (NORM) asm volatile("" ::"s"(a.norm));
   if constexpr (EPI == EPI_RESIDUAL) asm volatile("" ::"s"(a.res), "s"(a.ldr));
   const int b = blockIdx.x;
@@ -81,19 +89,25 @@ __global__ void __launch_bounds__(64 * WAVES) linear_kernel(const LinearArgs a) 
   const int lane = threadIdx.x & 63, col = lane & 15, g = lane >> 4;
   const int n0 = ct * 16 * NT;
 
+  // A lane's operand pointers for pair 0, half 0, and the element steps to pair p and half h
+  // (k = 64 p + 32 h): rows of k elements, or the MFMA-tiled layout (OPS = the layout bits of w
+  // and x, compile-time so that the steps are immediate offsets of the loads).
+  constexpr bool w_tiled = OPS & LAYOUT_W_TILED, x_tiled = OPS & LAYOUT_X_TILED;
+  constexpr int wsp = w_tiled ? 1024 : 64, wsh = w_tiled ? 512 : 32;
+  constexpr int xsp = x_tiled ? 1024 : 64, xsh = x_tiled ? 512 : 32;
   const uint16_t* wrow[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
-    const int r = (EPI == EPI_SILU_MUL && nb >= NT) ? a.up + n0 + 16 * (nb - NT) + col : n0 + 16 * nb + col;
-    wrow[nb] = a.w + (int64_t)r * a.ldw + 8 * g;
+    const int r = (EPI == EPI_SILU_MUL && nb >= NT) ? a.up + n0 + 16 * (nb - NT) : n0 + 16 * nb;
+    wrow[nb] = w_tiled ? a.w + (int64_t)(r >> 4) * a.kp * 1024 + 8 * lane : a.w + (int64_t)(r + col) * a.ldw + 8 * g;
   }
-  // Rows past the end read the last row: x row j only reaches output row j,
-  // which is not stored.
+  // Rows past the end read the last row (or a tiled x's padding rows): x row j only reaches
+  // output row j, which is not stored.
   const uint16_t* xrow[RB];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     const int row = min((rg * RB + rb) * 16 + col, a.rows - 1);
-    xrow[rb] = a.x + (int64_t)row * a.ldx + 8 * g;
+    xrow[rb] = x_tiled ? a.x + (int64_t)(rg * RB + rb) * a.kp * 1024 + 8 * lane : a.x + (int64_t)row * a.ldx + 8 * g;
   }
 
   constexpr int TILES = RB * NB, OUT = RB * NT;
@@ -127,7 +141,7 @@ __global__ void __launch_bounds__(64 * WAVES) linear_kernel(const LinearArgs a) 
       for (int h = 0; h < 2; ++h) {
         const int k = 64 * p + 32 * h;
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) wa[i][h][nb].u = *reinterpret_cast<const u32x4*>(wrow[nb] + k);
+        for (int nb = 0; nb < NB; ++nb) wa[i][h][nb].u = *reinterpret_cast<const u32x4*>(wrow[nb] + p * wsp + h * wsh);
       }
     }
   };
@@ -139,7 +153,7 @@ __global__ void __launch_bounds__(64 * WAVES) linear_kernel(const LinearArgs a) 
       for (int h = 0; h < 2; ++h) {
         const int k = 64 * p + 32 * h;
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) xa[i][h][rb].u = *reinterpret_cast<const u32x4*>(xrow[rb] + k);
+        for (int rb = 0; rb < RB; ++rb) xa[i][h][rb].u = *reinterpret_cast<const u32x4*>(xrow[rb] + p * xsp + h * xsh);
         gn[i][h].u = *reinterpret_cast<const u32x4*>(a.norm + k + 8 * g);
       }
     }
@@ -150,11 +164,10 @@ __global__ void __launch_bounds__(64 * WAVES) linear_kernel(const LinearArgs a) 
       if (p < a.kp) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const int k = 64 * p + 32 * h;
 #pragma unroll
-          for (int nb = 0; nb < NB; ++nb) wa[i][h][nb].u = *reinterpret_cast<const u32x4*>(wrow[nb] + k);
+          for (int nb = 0; nb < NB; ++nb) wa[i][h][nb].u = *reinterpret_cast<const u32x4*>(wrow[nb] + p * wsp + h * wsh);
 #pragma unroll
-          for (int rb = 0; rb < RB; ++rb) xa[i][h][rb].u = *reinterpret_cast<const u32x4*>(xrow[rb] + k);
+          for (int rb = 0; rb < RB; ++rb) xa[i][h][rb].u = *reinterpret_cast<const u32x4*>(xrow[rb] + p * xsp + h * xsh);
         }
       }
     }
@@ -283,8 +296,12 @@ __global__ void __launch_bounds__(64 * WAVES) linear_kernel(const LinearArgs a) 
 #pragma unroll
       for (int e = 0; e < 4; ++e) y[e] = round_bf16(y[e] / (1.f + expf(-y[e]))) * round_bf16(usum[o][e]);
     }
-    *reinterpret_cast<uint2*>(a.out + (int64_t)row * a.ldo + c) =
-        make_uint2(pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3]));
+    // a tiled out is the next projection's tiled x (k = n_out = a.up)
+    uint16_t* dst = (a.layout & LAYOUT_OUT_TILED)
+                        ? a.out + ((int64_t)(rg * RB + rb) * (a.up >> 6) + (c >> 6)) * 1024 + ((c >> 5) & 1) * 512 +
+                              (((c >> 3) & 3) * 16 + col) * 8 + (c & 7)
+                        : a.out + (int64_t)row * a.ldo + c;
+    *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3]));
   }
 }
 
@@ -318,38 +335,48 @@ Shape pick(int n_out, int kp, int epilogue) {
   return s;
 }
 
-template <int CH, int NT, int WAVES, int RB, int EPI, bool NORM>
+template <int CH, int NT, int WAVES, int RB, int EPI, bool NORM, int OPS>
 void launch_one(const LinearArgs& a, hipStream_t st) {
   const int groups = (a.n_tiles + 7) / 8;
   const unsigned blocks = (unsigned)groups * 8u * (unsigned)a.row_groups;
-  hipLaunchKernelGGL((linear_kernel<CH, NT, WAVES, RB, EPI, NORM>), dim3(blocks), dim3(64 * WAVES), 0, st, a);
+  hipLaunchKernelGGL((linear_kernel<CH, NT, WAVES, RB, EPI, NORM, OPS>), dim3(blocks), dim3(64 * WAVES), 0, st, a);
 }
 
-template <int NT, int WAVES, int RB, int EPI, bool NORM>
+template <int NT, int WAVES, int RB, int EPI, bool NORM, int OPS>
 void launch_ch(int ch, const LinearArgs& a, hipStream_t st) {
   if constexpr (NORM) {
-    if (ch == 1) launch_one<1, NT, WAVES, RB, EPI, NORM>(a, st);
-    else launch_one<MAX_NORM_CH, NT, WAVES, RB, EPI, NORM>(a, st);
+    if (ch == 1) launch_one<1, NT, WAVES, RB, EPI, NORM, OPS>(a, st);
+    else launch_one<MAX_NORM_CH, NT, WAVES, RB, EPI, NORM, OPS>(a, st);
   } else {
     switch (ch) {
-      case 1: launch_one<1, NT, WAVES, RB, EPI, NORM>(a, st); break;
-      case 2: launch_one<2, NT, WAVES, RB, EPI, NORM>(a, st); break;
-      case 3: launch_one<3, NT, WAVES, RB, EPI, NORM>(a, st); break;
-      case 4: launch_one<4, NT, WAVES, RB, EPI, NORM>(a, st); break;
+      case 1: launch_one<1, NT, WAVES, RB, EPI, NORM, OPS>(a, st); break;
+      case 2: launch_one<2, NT, WAVES, RB, EPI, NORM, OPS>(a, st); break;
+      case 3: launch_one<3, NT, WAVES, RB, EPI, NORM, OPS>(a, st); break;
+      case 4: launch_one<4, NT, WAVES, RB, EPI, NORM, OPS>(a, st); break;
       default:
-        if constexpr (EPI != EPI_SILU_MUL) launch_one<MAX_CH, NT, WAVES, RB, EPI, NORM>(a, st);
+        if constexpr (EPI != EPI_SILU_MUL) launch_one<MAX_CH, NT, WAVES, RB, EPI, NORM, OPS>(a, st);
         break;  // dkv_linear_supported rules out the rest
     }
   }
 }
 
+template <int EPI, bool NORM, int OPS>
+void launch_ops(const Shape& s, const LinearArgs& a, hipStream_t st) {
+  if constexpr (EPI == EPI_SILU_MUL) {
+    launch_ch<2, 8, 2, EPI, NORM, OPS>(s.ch, a, st);
+  } else {
+    if (s.nt == 2) launch_ch<2, 8, 1, EPI, NORM, OPS>(s.ch, a, st);
+    else launch_ch<1, 8, 1, EPI, NORM, OPS>(s.ch, a, st);
+  }
+}
+
 template <int EPI, bool NORM>
 void launch_epi(const Shape& s, const LinearArgs& a, hipStream_t st) {
-  if constexpr (EPI == EPI_SILU_MUL) {
-    launch_ch<2, 8, 2, EPI, NORM>(s.ch, a, st);
-  } else {
-    if (s.nt == 2) launch_ch<2, 8, 1, EPI, NORM>(s.ch, a, st);
-    else launch_ch<1, 8, 1, EPI, NORM>(s.ch, a, st);
+  switch (a.layout & (LAYOUT_W_TILED | LAYOUT_X_TILED)) {
+    case 0: launch_ops<EPI, NORM, 0>(s, a, st); break;
+    case LAYOUT_W_TILED: launch_ops<EPI, NORM, LAYOUT_W_TILED>(s, a, st); break;
+    case LAYOUT_X_TILED: launch_ops<EPI, NORM, LAYOUT_X_TILED>(s, a, st); break;
+    default: launch_ops<EPI, NORM, LAYOUT_W_TILED | LAYOUT_X_TILED>(s, a, st); break;
   }
 }
 
@@ -372,19 +399,22 @@ int dkv_linear_supported(int32_t rows, int32_t n, int32_t k, int32_t has_norm, i
   return 1;
 }
 
-int dkv_linear(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride, int32_t rows, int32_t n,
-               int32_t k, const void* norm_weight, float eps, int32_t epilogue, const void* residual,
-               int64_t residual_row_stride, void* out, int64_t out_row_stride, void* stream) {
+int dkv_linear_tiled(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride, int32_t rows,
+                     int32_t n, int32_t k, const void* norm_weight, float eps, int32_t epilogue, const void* residual,
+                     int64_t residual_row_stride, void* out, int64_t out_row_stride, int32_t layout, void* stream) {
   clear_error();
   const bool norm = norm_weight != nullptr;
   const int n_out = epilogue == EPI_SILU_MUL ? n / 2 : n;
+  // row strides of tiled operands are not used (their layout fixes every offset)
+  const bool wt = layout & LAYOUT_W_TILED, xt = layout & LAYOUT_X_TILED, ot = layout & LAYOUT_OUT_TILED;
   if (!x || !w || !out || !dkv_linear_supported(rows, n, k, norm, epilogue) || !al16(x) || !al16(w) ||
-      !al16(out) || (norm && !al16(norm_weight)) || (x_row_stride & 7) || (w_row_stride & 7) ||
-      (out_row_stride & 3) || x_row_stride < k || w_row_stride < k || out_row_stride < n_out ||
+      !al16(out) || (norm && !al16(norm_weight)) || (layout & ~7) || (ot && (n_out & 63)) ||
+      (!xt && ((x_row_stride & 7) || x_row_stride < k)) || (!wt && ((w_row_stride & 7) || w_row_stride < k)) ||
+      (!ot && ((out_row_stride & 3) || out_row_stride < n_out)) ||
       (epilogue == EPI_RESIDUAL &&
        (!residual || ((uintptr_t)residual & 7) || (residual_row_stride & 3) || residual_row_stride < n_out))) {
-    set_error("dkv_linear: unsupported or bad arguments (rows %d, n %d, k %d, epilogue %d; k a multiple of 64, "
-              "16-byte aligned bf16 rows)", rows, n, k, epilogue);
+    set_error("dkv_linear: unsupported or bad arguments (rows %d, n %d, k %d, epilogue %d, layout %d; k a multiple "
+              "of 64, 16-byte aligned bf16 rows, a tiled out n_out a multiple of 64)", rows, n, k, epilogue, layout);
     return DKV_EINVAL;
   }
   if (rows == 0) return 0;
@@ -406,12 +436,20 @@ int dkv_linear(const void* x, int64_t x_row_stride, const void* w, int64_t w_row
   a.n_tiles = n_out / (16 * s.nt);
   a.row_groups = (rows + 16 * s.rb - 1) / (16 * s.rb);
   a.up = n_out;
+  a.layout = layout;
   hipStream_t st = (hipStream_t)stream;
   if (epilogue == EPI_PLAIN) norm ? launch_epi<EPI_PLAIN, true>(s, a, st) : launch_epi<EPI_PLAIN, false>(s, a, st);
   else if (epilogue == EPI_RESIDUAL)
     norm ? launch_epi<EPI_RESIDUAL, true>(s, a, st) : launch_epi<EPI_RESIDUAL, false>(s, a, st);
   else norm ? launch_epi<EPI_SILU_MUL, true>(s, a, st) : launch_epi<EPI_SILU_MUL, false>(s, a, st);
   return (int)hipGetLastError();
+}
+
+int dkv_linear(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride, int32_t rows, int32_t n,
+               int32_t k, const void* norm_weight, float eps, int32_t epilogue, const void* residual,
+               int64_t residual_row_stride, void* out, int64_t out_row_stride, void* stream) {
+  return dkv_linear_tiled(x, x_row_stride, w, w_row_stride, rows, n, k, norm_weight, eps, epilogue, residual,
+                          residual_row_stride, out, out_row_stride, 0, stream);
 }
 
 }  // extern "C"

@@ -109,16 +109,62 @@ def linear_covered(rows, weight, norm=False, epilogue=LINEAR_PLAIN):
     return _weight_rows(weight) and _linear_supported(rows, weight.shape[0], weight.shape[1], int(norm), epilogue)
 
 
-def linear(x, weight, norm=None, eps=1e-6, residual=None, silu_mul=False):
+LINEAR_W_TILED, LINEAR_X_TILED, LINEAR_OUT_TILED = 1, 2, 4
+
+
+def mfma_tiled(t):
+    """A copy of the bf16 matrix t [R, k] (k a multiple of 64) in dkv_linear's MFMA-tiled layout,
+    rows rounded up to 16 with zeros: element (r, c) at ((r // 16) * (k // 64) + c // 64) * 1024
+    + (c // 32 % 2) * 512 + ((c // 8 % 4) * 16 + r % 16) * 8 + c % 8, the order in which the
+    kernel's lanes read a 16-row x 64-column block, so that each of its load instructions reads
+    1 KB of consecutive bytes. Returned as a contiguous [R16, k] tensor."""
+    R, k = t.shape
+    R16 = (R + 15) // 16 * 16
+    if R16 != R:
+        t = torch.cat((t, t.new_zeros(R16 - R, k)))
+    return t.reshape(R16 // 16, 16, k // 64, 2, 4, 8).permute(0, 2, 3, 4, 1, 5).contiguous().view(R16, k)
+
+
+def mfma_untiled(t, rows):
+    """The first `rows` rows of a matrix held in the MFMA-tiled layout (mfma_tiled's inverse)."""
+    R16, k = t.shape
+    return t.view(R16 // 16, k // 64, 2, 4, 16, 8).permute(0, 4, 1, 2, 3, 5).reshape(R16, k)[:rows]
+
+
+def linear(x, weight, norm=None, eps=1e-6, residual=None, silu_mul=False, weight_tiled=None, x_tiled=False,
+           out_tiled=False, rows=None):
     """x [..., k] . weight[n, k]^T in one launch, optionally with RMSNorm(x) * norm first and the
     residual add (out = residual + y) or SiLU*up over [gate | up] weight rows after; the rounding
-    points are the torch compositions'. Returns None when the kernel does not cover the inputs."""
+    points are the torch compositions'. Returns None when the kernel does not cover the inputs.
+
+    weight_tiled: mfma_tiled(weight), read instead of weight (same results). x_tiled: x is a
+    [rows rounded up to 16, k] matrix in the tiled layout, `rows` its row count. out_tiled: the
+    output is returned in the tiled layout ([rows rounded up to 16, n_out], padding rows not
+    written), as the x of a following x_tiled call."""
     epi = LINEAR_SILU_MUL if silu_mul else (LINEAR_RESIDUAL if residual is not None else LINEAR_PLAIN)
     if not _fused(x) or not _weight_rows(weight) or x.shape[-1] != weight.shape[1]:
         return None
-    x2 = _rows(x)
-    rows, k = x2.shape
+    layout = 0
+    if weight_tiled is not None:
+        if not (_fused(weight_tiled) and weight_tiled.is_contiguous() and weight_tiled.shape == weight.shape
+                and weight_tiled.data_ptr() % 16 == 0):
+            return None
+        layout |= LINEAR_W_TILED
+    if x_tiled:
+        if rows is None or x.dim() != 2 or not x.is_contiguous() or x.shape[0] != (rows + 15) // 16 * 16 \
+                or x.data_ptr() % 16:
+            return None
+        x2 = x
+        layout |= LINEAR_X_TILED
+    else:
+        x2 = _rows(x)
+        rows = x2.shape[0]
+    k = x2.shape[1]
     n_out = weight.shape[0] // 2 if silu_mul else weight.shape[0]
+    if out_tiled:
+        if n_out % 64:
+            return None
+        layout |= LINEAR_OUT_TILED
     if norm is not None and (not _fused(norm) or norm.dim() != 1 or norm.shape[0] != k or norm.stride(0) != 1
                              or norm.data_ptr() % 16):
         return None
@@ -131,13 +177,16 @@ def linear(x, weight, norm=None, eps=1e-6, residual=None, silu_mul=False):
             return None
     if not _linear_supported(rows, weight.shape[0], k, int(norm is not None), epi):
         return None
-    out = torch.empty((rows, n_out), dtype=x.dtype, device=x.device)
-    _lib.check(_lib.load().dkv_linear(
-        x2.data_ptr(), x2.stride(0), weight.data_ptr(), weight.stride(0), rows, weight.shape[0], k,
+    out = torch.empty(((rows + 15) // 16 * 16 if out_tiled else rows, n_out), dtype=x.dtype, device=x.device)
+    w = weight if weight_tiled is None else weight_tiled
+    _lib.check(_lib.load().dkv_linear_tiled(
+        x2.data_ptr(), x2.stride(0), w.data_ptr(), w.stride(0), rows, weight.shape[0], k,
         None if norm is None else norm.data_ptr(), float(eps), epi, None if r2 is None else r2.data_ptr(),
-        0 if r2 is None else r2.stride(0), out.data_ptr(), out.stride(0), _lib.stream_handle(x.device)),
+        0 if r2 is None else r2.stride(0), out.data_ptr(), out.stride(0), layout, _lib.stream_handle(x.device)),
         'dkv_linear')
-    return out.view(*x.shape[:-1], n_out)
+    if out_tiled:
+        return out
+    return out.view(*(x.shape[:-1] if not x_tiled else (rows,)), n_out)
 
 
 class _LayerPlan:
@@ -158,6 +207,35 @@ class _LayerPlan:
                 and self.d_w is mlp._modules['down_proj']._parameters['weight']
                 and self.ln1_w is m['input_layernorm']._parameters['weight']
                 and self.ln2_w is m['post_attention_layernorm']._parameters['weight'])
+
+
+def _layer_tiles(layer, p):
+    """mfma_tiled copies of the layer's four projection weights (Q/K/V, o_proj, gate/up,
+    down_proj), which its dkv_linear launches read instead of the row-major weights (the same
+    results; each load instruction then reads 1 KB of consecutive bytes). One set per layer, shared
+    by its plans, made again (into the same memory, so that graphs captured earlier read the new
+    values on their next replay) when a weight's storage or version counter has changed. None when
+    a graph is being captured and no current copies exist: allocating them inside the capture would
+    tie them to it, and the launches then read the row-major weights."""
+    ws = (p.qkv_w, p.o_w, p.gu_w, p.d_w)
+    key = tuple((w.data_ptr(), w._version) for w in ws)
+    cur = layer.__dict__.get('_dkv_tiles')
+    if cur is not None and all(a is b for a, b in zip(cur[0], ws)):
+        if cur[1] == key:
+            return cur[2]
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        with torch.no_grad():
+            for t, w in zip(cur[2], ws):
+                t.copy_(mfma_tiled(w))
+        layer.__dict__['_dkv_tiles'] = (ws, key, cur[2])
+        return cur[2]
+    if torch.cuda.is_current_stream_capturing():
+        return None
+    with torch.no_grad():
+        tiles = tuple(mfma_tiled(w) for w in ws)
+    layer.__dict__['_dkv_tiles'] = (ws, key, tiles)
+    return tiles
 
 
 def _layer_plan(layer, n, width):
@@ -202,7 +280,7 @@ def _layer_plan(layer, n, width):
     return p
 
 
-def _fused_layer_eager(p, h, n, cache, cos, sin):
+def _fused_layer_eager(p, tiles, h, n, cache, cos, sin):
     """The fused layer's eager launches for a checked plan: the launches and arguments linear() and
     attend_projection() would make, without their per-call checks (which cost more host time than
     the GPU spends on a 64-token chunk). The intermediates (the joined projection, q | k | v, the
@@ -216,25 +294,32 @@ def _fused_layer_eager(p, h, n, cache, cos, sin):
     ow, old, orows, ok = p.o_args
     gw, gld, grows, gk = p.gu_args
     dw, dld, drows, dk = p.d_args
-    # element offsets of [qkv | q,k,v | attention out | h2 | act], each n rows (multiples of 64 columns)
+    wl = gl = dl = 0  # dkv_linear_tiled layouts: Q/K/V and o_proj, gate/up, down_proj
+    if tiles is not None:
+        (qw, ow, gw, dw), qld, old, gld, dld = tiles, qk, ok, gk, dk
+        wl = gl = dl = LINEAR_W_TILED
+        if inter % 64 == 0:  # SiLU*up goes to down_proj in the tiled layout
+            gl, dl = LINEAR_W_TILED | LINEAR_OUT_TILED, LINEAR_W_TILED | LINEAR_X_TILED
+    # element offsets of [qkv | q,k,v | attention out | h2 | act], each n rows (multiples of 64
+    # columns; act in rows rounded up to 16 when tiled)
     o_qkvo = n * qrows
     o_att = o_qkvo + n * qrows
     o_h2 = o_att + n * ok
     o_act = o_h2 + n * orows
-    scratch = torch.empty(o_act + n * inter, dtype=torch.bfloat16, device=h.device)
+    scratch = torch.empty(o_act + (n + 15) // 16 * 16 * inter, dtype=torch.bfloat16, device=h.device)
     out = torch.empty((1, n, drows), dtype=torch.bfloat16, device=h.device)
     base = scratch.data_ptr()
     xp, qkv, att, h2, act = h.data_ptr(), base, base + 2 * o_att, base + 2 * o_h2, base + 2 * o_act
-    _lib.check(lib.dkv_linear(xp, width, qw.data_ptr(), qld, n, qrows, qk, p.ln1_w.data_ptr(), p.eps1, LINEAR_PLAIN,
-                              None, 0, qkv, qrows, stream), 'dkv_linear')
+    _lib.check(lib.dkv_linear_tiled(xp, width, qw.data_ptr(), qld, n, qrows, qk, p.ln1_w.data_ptr(), p.eps1,
+                                    LINEAR_PLAIN, None, 0, qkv, qrows, wl, stream), 'dkv_linear')
     cache._fused_attention(n, p.q_heads, p.layer_idx, qkv, qrows, cos.data_ptr(), sin.data_ptr(), cos.stride(0),
                            base + 2 * o_qkvo, att, stream)
-    _lib.check(lib.dkv_linear(att, ok, ow.data_ptr(), old, n, orows, ok, None, 1e-6, LINEAR_RESIDUAL, xp, width,
-                              h2, orows, stream), 'dkv_linear')
-    _lib.check(lib.dkv_linear(h2, width, gw.data_ptr(), gld, n, grows, gk, p.ln2_w.data_ptr(), p.eps2,
-                              LINEAR_SILU_MUL, None, 0, act, inter, stream), 'dkv_linear')
-    _lib.check(lib.dkv_linear(act, inter, dw.data_ptr(), dld, n, drows, dk, None, 1e-6, LINEAR_RESIDUAL, h2, width,
-                              out.data_ptr(), drows, stream), 'dkv_linear')
+    _lib.check(lib.dkv_linear_tiled(att, ok, ow.data_ptr(), old, n, orows, ok, None, 1e-6, LINEAR_RESIDUAL, xp,
+                                    width, h2, orows, wl, stream), 'dkv_linear')
+    _lib.check(lib.dkv_linear_tiled(h2, width, gw.data_ptr(), gld, n, grows, gk, p.ln2_w.data_ptr(), p.eps2,
+                                    LINEAR_SILU_MUL, None, 0, act, inter, gl, stream), 'dkv_linear')
+    _lib.check(lib.dkv_linear_tiled(act, inter, dw.data_ptr(), dld, n, drows, dk, None, 1e-6, LINEAR_RESIDUAL, h2,
+                                    width, out.data_ptr(), drows, dl, stream), 'dkv_linear')
     return out
 
 
@@ -254,20 +339,24 @@ def fused_decoder_layer(layer, hidden_states, cache, position_embeddings):
     p = _layer_plan(layer, n, width)
     if p is None:
         return None
+    tiles = _layer_tiles(layer, p)
     if p.eager_ok and p.kv_heads == cache.heads and cache._graph is None and cache.chunk_segments is None:
         cos, sin = position_embeddings
         if (h.is_contiguous() and h.data_ptr() % 16 == 0 and cos.shape == (1, n, 64) and sin.shape == cos.shape
                 and cos.dtype == torch.bfloat16 and sin.dtype == torch.bfloat16 and cos.is_contiguous()
                 and sin.is_contiguous() and cos.data_ptr() % 16 == 0 and sin.data_ptr() % 16 == 0):
-            return _fused_layer_eager(p, h, n, cache, cos.view(n, 64), sin.view(n, 64))
+            return _fused_layer_eager(p, tiles, h, n, cache, cos.view(n, 64), sin.view(n, 64))
     ln1, ln2 = layer.input_layernorm, layer.post_attention_layernorm
     o_w, d_w = attn.o_proj.weight, mlp.down_proj.weight
     x = h.reshape(n, width)
-    qkv = linear(x, attn._qkv_weight, norm=ln1.weight, eps=ln1.variance_epsilon)
+    qt, ot, gt, dt = tiles if tiles is not None else (None,) * 4
+    qkv = linear(x, attn._qkv_weight, norm=ln1.weight, eps=ln1.variance_epsilon, weight_tiled=qt)
     o = attend_projection(attn, cache, qkv.view(1, n, -1), position_embeddings)
-    h2 = linear(o.view(n, -1), o_w, residual=x)
-    act = linear(h2, mlp._gate_up_weight, norm=ln2.weight, eps=ln2.variance_epsilon, silu_mul=True)
-    return linear(act, d_w, residual=h2).view(1, n, width)
+    h2 = linear(o.view(n, -1), o_w, residual=x, weight_tiled=ot)
+    act_tiled = tiles is not None and p.inter % 64 == 0  # SiLU*up to down_proj in the tiled layout
+    act = linear(h2, mlp._gate_up_weight, norm=ln2.weight, eps=ln2.variance_epsilon, silu_mul=True,
+                 weight_tiled=gt, out_tiled=act_tiled)
+    return linear(act, d_w, residual=h2, weight_tiled=dt, x_tiled=act_tiled, rows=n).view(1, n, width)
 
 
 def install_fused_ops(text, state):

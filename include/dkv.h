@@ -307,6 +307,27 @@ int dkv_linear(const void* x, int64_t x_row_stride, const void* w, int64_t w_row
                int32_t epilogue, const void* residual, int64_t residual_row_stride,
                void* out, int64_t out_row_stride, void* stream);
 
+/* dkv_linear with operands in the MFMA-tiled layout, which has no counterpart
+ * in the reference (its projections are library GEMMs over row-major weights):
+ * a layout for callers that keep a second copy of each weight (and of the
+ * SiLU*up intermediate) so that every load instruction of the kernel reads
+ * 1 KB of consecutive bytes. Element (r, c) of a tiled [R, K] matrix (R a
+ * multiple of 16, rows past `rows` being padding) sits at
+ *   ((r / 16) * (K / 64) + c / 64) * 1024 + (c / 32 % 2) * 512
+ *     + ((c / 8 % 4) * 16 + r % 16) * 8 + c % 8.
+ * layout bits: DKV_LINEAR_W_TILED (w, K = k), DKV_LINEAR_X_TILED (x, K = k,
+ * rows rounded up to 16), DKV_LINEAR_OUT_TILED (out, K = n_out, a multiple of
+ * 64; its padding rows are not written). The row stride of a tiled operand is
+ * ignored. The results are bit-identical to dkv_linear's; layout 0 is
+ * dkv_linear. */
+#define DKV_LINEAR_W_TILED 1
+#define DKV_LINEAR_X_TILED 2
+#define DKV_LINEAR_OUT_TILED 4
+int dkv_linear_tiled(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride,
+                     int32_t rows, int32_t n, int32_t k, const void* norm_weight, float eps,
+                     int32_t epilogue, const void* residual, int64_t residual_row_stride,
+                     void* out, int64_t out_row_stride, int32_t layout, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -97,6 +97,32 @@ def test_linear_matches_torch_composition(cuda, rows, k, n, norm, epi):
     check(got.cpu(), yt.cpu(), 2 * extra)
 
 
+@pytest.mark.parametrize('rows', [1, 17, 64, 100])
+@pytest.mark.parametrize('k,n,norm,epi', SHAPES)
+def test_tiled_layouts_equal_row_major(cuda, rows, k, n, norm, epi):
+    """dkv_linear_tiled reads the MFMA-tiled copies of w (and of x) and writes a tiled out: every lane
+    loads the same values as from the row-major operands, so every output bit is the same."""
+    announce(f'linear tiled: rows={rows} k={k} n={n} norm={norm} epi={epi}')
+    g = torch.Generator().manual_seed(rows * 5 + k + n)
+    x = (torch.randn(rows, k, generator=g) * 2).to(BF).to(cuda)
+    w = (torch.randn(n, k, generator=g) / k ** 0.5).to(BF).to(cuda)
+    nw = (torch.rand(k, generator=g) + 0.5).to(BF).to(cuda) if norm else None
+    n_out = n // 2 if epi == 'silu' else n
+    res = (torch.randn(rows, n_out, generator=g)).to(BF).to(cuda) if epi == 'residual' else None
+    kw = dict(norm=nw, eps=1e-5, residual=res, silu_mul=epi == 'silu')
+    want = gpu_ops.linear(x, w, **kw)
+    wt = gpu_ops.mfma_tiled(w)
+    xt = gpu_ops.mfma_tiled(x)
+    assert torch.equal(gpu_ops.linear(x, w, weight_tiled=wt, **kw), want)
+    assert torch.equal(gpu_ops.linear(xt, w, x_tiled=True, rows=rows, **kw), want)
+    assert torch.equal(gpu_ops.linear(xt, w, weight_tiled=wt, x_tiled=True, rows=rows, **kw), want)
+    if n_out % 64 == 0:
+        got = gpu_ops.linear(x, w, weight_tiled=wt, out_tiled=True, **kw)
+        assert got.shape == ((rows + 15) // 16 * 16, n_out)
+        assert torch.equal(gpu_ops.mfma_untiled(got, rows), want)
+    torch.cuda.synchronize()
+
+
 def test_linear_strided_rows_and_uncovered_inputs(cuda):
     announce('linear: strided x, uncovered inputs')
     g = torch.Generator().manual_seed(5)
