@@ -169,8 +169,9 @@ def test_fused_layers_match_upstream_layers(cuda):
 def test_eager_fused_layers_follow_weight_changes(cuda):
     """The eager fused layers check a layer once per chunk length and keep its weight objects, reading
     their data pointers at every call: a weight whose storage moves (param.data replaced, as
-    Module.to() does) and a weight replaced by a new Parameter are both used by the next forward.
-    Logits change and stay within 0.05 of the upstream layers with the new weights."""
+    Module.to() does), a weight replaced by a new Parameter and a weight changed in place are all
+    used by the next forward (the layer's MFMA-tiled weight copies are made again). Logits change
+    and stay within 0.05 of the upstream layers with the new weights."""
     announce('linear: eager fused layers follow weight changes')
     from dkv.streaming import StreamingDecoder, build_decoder
     model = build_decoder(layers=2, hidden=384, heads=6, kv_heads=2, intermediate=768, vocab=512, seed=23)
@@ -207,3 +208,13 @@ def test_eager_fused_layers_follow_weight_changes(cuda):
     print(f'[fused-weights] change {changed:.3e}, fused vs upstream {diff:.3e}', flush=True)
     assert changed > 1e-2, changed
     assert diff <= 0.05, diff
+    # an in-place change of a joined weight (through its q_proj view: one version counter) makes the
+    # next forward tile the layer's weight copies again
+    with torch.no_grad():
+        layer.self_attn.q_proj.weight.mul_(1.5)
+    fused2, upstream2 = logits(True), logits(False)
+    changed2 = (fused2 - fused).abs().max().item()
+    diff2 = (fused2 - upstream2).abs().max().item()
+    print(f'[fused-weights] in place: change {changed2:.3e}, fused vs upstream {diff2:.3e}', flush=True)
+    assert changed2 > 1e-2, changed2
+    assert diff2 <= 0.05, diff2
