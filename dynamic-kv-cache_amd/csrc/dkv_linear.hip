@@ -61,7 +61,17 @@ struct LinearArgs {  // passed by value and never written (a written copy would 
 // at ((r / 16) * kp + c / 64) * 1024 + (c / 32 % 2) * 512 + ((c / 8 % 4) * 16 + r % 16) * 8 + c % 8),
 // so that each 16-byte-per-lane load instruction reads 1 KB of consecutive bytes (8 full cache
 // lines instead of 64-byte halves of 16). A tiled x or out has its rows rounded up to 16.
-enum { LAYOUT_W_TILED = DKV_LINEAR_W_TILED, LAYOUT_X_TILED = DKV_LINEAR_X_TILED, LAYOUT_OUT_TILED = DKV_LINEAR_OUT_TILED };
+enum {
+  LAYOUT_W_TILED = DKV_LINEAR_W_TILED,
+  LAYOUT_X_TILED = DKV_LINEAR_X_TILED,
+  LAYOUT_OUT_TILED = DKV_LINEAR_OUT_TILED,
+  LAYOUT_RES_TILED = DKV_LINEAR_RES_TILED
+};
+
+// Offset of element (r, c) of a tiled matrix with kp pairs of 64 columns per row.
+__device__ __forceinline__ int64_t tiled_offset(int r, int c, int kp) {
+  return ((int64_t)(r >> 4) * kp + (c >> 6)) * 1024 + ((c >> 5) & 1) * 512 + (((c >> 3) & 3) * 16 + (r & 15)) * 8 + (c & 7);
+}
 
 __device__ __forceinline__ float lane_group_sum(float x) {
   // sum over lanes col, col + 16, col + 32, col + 48 (gfx950 lane swaps)
@@ -119,8 +129,11 @@ __global__ void __launch_bounds__(64 * WAVES) linear_kernel(const LinearArgs a) 
 #pragma unroll
     for (int o = 0; o < OUT; ++o) {
       if (o % WAVES != wave) continue;
-      const int row = min((rg * RB + o / NT) * 16 + col, a.rows - 1);
-      resv[o] = *reinterpret_cast<const uint2*>(a.res + (int64_t)row * a.ldr + n0 + 16 * (o % NT) + 4 * g);
+      const int row = min((rg * RB + o / NT) * 16 + col, a.rows - 1), c = n0 + 16 * (o % NT) + 4 * g;
+      // a tiled residual has its rows rounded up to 16: row (rg * RB + o / NT) * 16 + col is there
+      resv[o] = *reinterpret_cast<const uint2*>(
+          a.res + ((a.layout & LAYOUT_RES_TILED) ? tiled_offset((rg * RB + o / NT) * 16 + col, c, a.up >> 6)
+                                                 : (int64_t)row * a.ldr + c));
     }
   }
 
@@ -297,10 +310,7 @@ __global__ void __launch_bounds__(64 * WAVES) linear_kernel(const LinearArgs a) 
       for (int e = 0; e < 4; ++e) y[e] = round_bf16(y[e] / (1.f + expf(-y[e]))) * round_bf16(usum[o][e]);
     }
     // a tiled out is the next projection's tiled x (k = n_out = a.up)
-    uint16_t* dst = (a.layout & LAYOUT_OUT_TILED)
-                        ? a.out + ((int64_t)(rg * RB + rb) * (a.up >> 6) + (c >> 6)) * 1024 + ((c >> 5) & 1) * 512 +
-                              (((c >> 3) & 3) * 16 + col) * 8 + (c & 7)
-                        : a.out + (int64_t)row * a.ldo + c;
+    uint16_t* dst = a.out + ((a.layout & LAYOUT_OUT_TILED) ? tiled_offset(row, c, a.up >> 6) : (int64_t)row * a.ldo + c);
     *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3]));
   }
 }
@@ -407,14 +417,17 @@ int dkv_linear_tiled(const void* x, int64_t x_row_stride, const void* w, int64_t
   const int n_out = epilogue == EPI_SILU_MUL ? n / 2 : n;
   // row strides of tiled operands are not used (their layout fixes every offset)
   const bool wt = layout & LAYOUT_W_TILED, xt = layout & LAYOUT_X_TILED, ot = layout & LAYOUT_OUT_TILED;
+  const bool rt = layout & LAYOUT_RES_TILED;
   if (!x || !w || !out || !dkv_linear_supported(rows, n, k, norm, epilogue) || !al16(x) || !al16(w) ||
-      !al16(out) || (norm && !al16(norm_weight)) || (layout & ~7) || (ot && (n_out & 63)) ||
+      !al16(out) || (norm && !al16(norm_weight)) || (layout & ~15) || ((ot || rt) && (n_out & 63)) ||
+      (rt && epilogue != EPI_RESIDUAL) ||
       (!xt && ((x_row_stride & 7) || x_row_stride < k)) || (!wt && ((w_row_stride & 7) || w_row_stride < k)) ||
       (!ot && ((out_row_stride & 3) || out_row_stride < n_out)) ||
       (epilogue == EPI_RESIDUAL &&
-       (!residual || ((uintptr_t)residual & 7) || (residual_row_stride & 3) || residual_row_stride < n_out))) {
+       (!residual || ((uintptr_t)residual & 7) || (!rt && ((residual_row_stride & 3) || residual_row_stride < n_out))))) {
     set_error("dkv_linear: unsupported or bad arguments (rows %d, n %d, k %d, epilogue %d, layout %d; k a multiple "
-              "of 64, 16-byte aligned bf16 rows, a tiled out n_out a multiple of 64)", rows, n, k, epilogue, layout);
+              "of 64, 16-byte aligned bf16 rows, a tiled out or residual n_out a multiple of 64)", rows, n, k,
+              epilogue, layout);
     return DKV_EINVAL;
   }
   if (rows == 0) return 0;

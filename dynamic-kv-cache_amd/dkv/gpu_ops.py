@@ -109,7 +109,7 @@ def linear_covered(rows, weight, norm=False, epilogue=LINEAR_PLAIN):
     return _weight_rows(weight) and _linear_supported(rows, weight.shape[0], weight.shape[1], int(norm), epilogue)
 
 
-LINEAR_W_TILED, LINEAR_X_TILED, LINEAR_OUT_TILED = 1, 2, 4
+LINEAR_W_TILED, LINEAR_X_TILED, LINEAR_OUT_TILED, LINEAR_RES_TILED = 1, 2, 4, 8
 
 
 def mfma_tiled(t):
@@ -132,7 +132,7 @@ def mfma_untiled(t, rows):
 
 
 def linear(x, weight, norm=None, eps=1e-6, residual=None, silu_mul=False, weight_tiled=None, x_tiled=False,
-           out_tiled=False, rows=None):
+           out_tiled=False, rows=None, residual_tiled=False):
     """x [..., k] . weight[n, k]^T in one launch, optionally with RMSNorm(x) * norm first and the
     residual add (out = residual + y) or SiLU*up over [gate | up] weight rows after; the rounding
     points are the torch compositions'. Returns None when the kernel does not cover the inputs.
@@ -140,7 +140,8 @@ def linear(x, weight, norm=None, eps=1e-6, residual=None, silu_mul=False, weight
     weight_tiled: mfma_tiled(weight), read instead of weight (same results). x_tiled: x is a
     [rows rounded up to 16, k] matrix in the tiled layout, `rows` its row count. out_tiled: the
     output is returned in the tiled layout ([rows rounded up to 16, n_out], padding rows not
-    written), as the x of a following x_tiled call."""
+    written), as the x of a following x_tiled call. residual_tiled: the residual is such a tiled
+    [rows rounded up to 16, n_out] matrix."""
     epi = LINEAR_SILU_MUL if silu_mul else (LINEAR_RESIDUAL if residual is not None else LINEAR_PLAIN)
     if not _fused(x) or not _weight_rows(weight) or x.shape[-1] != weight.shape[1]:
         return None
@@ -172,9 +173,16 @@ def linear(x, weight, norm=None, eps=1e-6, residual=None, silu_mul=False, weight
     if residual is not None:
         if not _fused(residual) or residual.shape[-1] != n_out:
             return None
-        r2 = residual.reshape(-1, n_out)
-        if r2.shape[0] != rows or r2.stride(-1) != 1 or r2.stride(0) % 4 or r2.data_ptr() % 8:
-            return None
+        if residual_tiled:
+            if n_out % 64 or residual.shape != ((rows + 15) // 16 * 16, n_out) or not residual.is_contiguous() \
+                    or residual.data_ptr() % 16:
+                return None
+            r2 = residual
+            layout |= LINEAR_RES_TILED
+        else:
+            r2 = residual.reshape(-1, n_out)
+            if r2.shape[0] != rows or r2.stride(-1) != 1 or r2.stride(0) % 4 or r2.data_ptr() % 8:
+                return None
     if not _linear_supported(rows, weight.shape[0], k, int(norm is not None), epi):
         return None
     out = torch.empty(((rows + 15) // 16 * 16 if out_tiled else rows, n_out), dtype=x.dtype, device=x.device)
@@ -294,28 +302,34 @@ def _fused_layer_eager(p, tiles, h, n, cache, cos, sin):
     ow, old, orows, ok = p.o_args
     gw, gld, grows, gk = p.gu_args
     dw, dld, drows, dk = p.d_args
-    wl = gl = dl = 0  # dkv_linear_tiled layouts: Q/K/V and o_proj, gate/up, down_proj
+    ql = ol = gl = dl = 0  # dkv_linear_tiled layouts of Q/K/V, o_proj, gate/up, down_proj
     if tiles is not None:
         (qw, ow, gw, dw), qld, old, gld, dld = tiles, qk, ok, gk, dk
-        wl = gl = dl = LINEAR_W_TILED
+        ql = ol = gl = dl = LINEAR_W_TILED
         if inter % 64 == 0:  # SiLU*up goes to down_proj in the tiled layout
-            gl, dl = LINEAR_W_TILED | LINEAR_OUT_TILED, LINEAR_W_TILED | LINEAR_X_TILED
+            gl |= LINEAR_OUT_TILED
+            dl |= LINEAR_X_TILED
+        if orows % 64 == 0:  # and the post-attention residual h2 to gate/up and down_proj
+            ol |= LINEAR_OUT_TILED
+            gl |= LINEAR_X_TILED
+            dl |= LINEAR_RES_TILED
     # element offsets of [qkv | q,k,v | attention out | h2 | act], each n rows (multiples of 64
     # columns; act in rows rounded up to 16 when tiled)
     o_qkvo = n * qrows
     o_att = o_qkvo + n * qrows
     o_h2 = o_att + n * ok
-    o_act = o_h2 + n * orows
-    scratch = torch.empty(o_act + (n + 15) // 16 * 16 * inter, dtype=torch.bfloat16, device=h.device)
+    n16 = (n + 15) // 16 * 16
+    o_act = o_h2 + n16 * orows
+    scratch = torch.empty(o_act + n16 * inter, dtype=torch.bfloat16, device=h.device)
     out = torch.empty((1, n, drows), dtype=torch.bfloat16, device=h.device)
     base = scratch.data_ptr()
     xp, qkv, att, h2, act = h.data_ptr(), base, base + 2 * o_att, base + 2 * o_h2, base + 2 * o_act
     _lib.check(lib.dkv_linear_tiled(xp, width, qw.data_ptr(), qld, n, qrows, qk, p.ln1_w.data_ptr(), p.eps1,
-                                    LINEAR_PLAIN, None, 0, qkv, qrows, wl, stream), 'dkv_linear')
+                                    LINEAR_PLAIN, None, 0, qkv, qrows, ql, stream), 'dkv_linear')
     cache._fused_attention(n, p.q_heads, p.layer_idx, qkv, qrows, cos.data_ptr(), sin.data_ptr(), cos.stride(0),
                            base + 2 * o_qkvo, att, stream)
     _lib.check(lib.dkv_linear_tiled(att, ok, ow.data_ptr(), old, n, orows, ok, None, 1e-6, LINEAR_RESIDUAL, xp,
-                                    width, h2, orows, wl, stream), 'dkv_linear')
+                                    width, h2, orows, ol, stream), 'dkv_linear')
     _lib.check(lib.dkv_linear_tiled(h2, width, gw.data_ptr(), gld, n, grows, gk, p.ln2_w.data_ptr(), p.eps2,
                                     LINEAR_SILU_MUL, None, 0, act, inter, gl, stream), 'dkv_linear')
     _lib.check(lib.dkv_linear_tiled(act, inter, dw.data_ptr(), dld, n, drows, dk, None, 1e-6, LINEAR_RESIDUAL, h2,
@@ -352,11 +366,14 @@ def fused_decoder_layer(layer, hidden_states, cache, position_embeddings):
     qt, ot, gt, dt = tiles if tiles is not None else (None,) * 4
     qkv = linear(x, attn._qkv_weight, norm=ln1.weight, eps=ln1.variance_epsilon, weight_tiled=qt)
     o = attend_projection(attn, cache, qkv.view(1, n, -1), position_embeddings)
-    h2 = linear(o.view(n, -1), o_w, residual=x, weight_tiled=ot)
-    act_tiled = tiles is not None and p.inter % 64 == 0  # SiLU*up to down_proj in the tiled layout
+    # SiLU*up to down_proj, and h2 to gate/up and down_proj, in the tiled layout
+    act_tiled = tiles is not None and p.inter % 64 == 0
+    h2_tiled = tiles is not None and width % 64 == 0
+    h2 = linear(o.view(n, -1), o_w, residual=x, weight_tiled=ot, out_tiled=h2_tiled)
     act = linear(h2, mlp._gate_up_weight, norm=ln2.weight, eps=ln2.variance_epsilon, silu_mul=True,
-                 weight_tiled=gt, out_tiled=act_tiled)
-    return linear(act, d_w, residual=h2, weight_tiled=dt, x_tiled=act_tiled, rows=n).view(1, n, width)
+                 weight_tiled=gt, x_tiled=h2_tiled, out_tiled=act_tiled, rows=n)
+    return linear(act, d_w, residual=h2, weight_tiled=dt, x_tiled=act_tiled, rows=n,
+                  residual_tiled=h2_tiled).view(1, n, width)
 
 
 def install_fused_ops(text, state):

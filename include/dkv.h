@@ -317,12 +317,14 @@ int dkv_linear(const void* x, int64_t x_row_stride, const void* w, int64_t w_row
  *     + ((c / 8 % 4) * 16 + r % 16) * 8 + c % 8.
  * layout bits: DKV_LINEAR_W_TILED (w, K = k), DKV_LINEAR_X_TILED (x, K = k,
  * rows rounded up to 16), DKV_LINEAR_OUT_TILED (out, K = n_out, a multiple of
- * 64; its padding rows are not written). The row stride of a tiled operand is
- * ignored. The results are bit-identical to dkv_linear's; layout 0 is
- * dkv_linear. */
+ * 64; its padding rows are not written), DKV_LINEAR_RES_TILED (the residual of
+ * DKV_LINEAR_RESIDUAL, K = n_out, a multiple of 64, rows rounded up to 16).
+ * The row stride of a tiled operand is ignored. The results are bit-identical
+ * to dkv_linear's; layout 0 is dkv_linear. */
 #define DKV_LINEAR_W_TILED 1
 #define DKV_LINEAR_X_TILED 2
 #define DKV_LINEAR_OUT_TILED 4
+#define DKV_LINEAR_RES_TILED 8
 int dkv_linear_tiled(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride,
                      int32_t rows, int32_t n, int32_t k, const void* norm_weight, float eps,
                      int32_t epilogue, const void* residual, int64_t residual_row_stride,

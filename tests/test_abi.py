@@ -354,6 +354,9 @@ def test_linear_rejects_unsupported_shapes_without_touching_the_device():
                           None) == _lib.DKV_EINVAL  # misaligned x
     assert lib.dkv_linear(ok, 960, ok, 960, 0, 960, 960, None, 1e-5, 0, None, 0, ok, 960, None) == 0  # no rows
     # dkv_linear_tiled: undefined layout bits, a tiled out whose n_out is not a multiple of 64
+    assert lib.dkv_linear_tiled(ok, 960, ok, 960, 64, 960, 960, None, 1e-5, 0, None, 0, ok, 960, 16,
+                                None) == _lib.DKV_EINVAL
+    # a tiled residual needs the residual epilogue
     assert lib.dkv_linear_tiled(ok, 960, ok, 960, 64, 960, 960, None, 1e-5, 0, None, 0, ok, 960, 8,
                                 None) == _lib.DKV_EINVAL
     assert lib.dkv_linear_tiled(ok, 960, ok, 960, 64, 976, 960, None, 1e-5, 0, None, 0, ok, 976, 4,
@@ -361,3 +364,4 @@ def test_linear_rejects_unsupported_shapes_without_touching_the_device():
     assert 'layout' in lib.dkv_last_error().decode()
     # row strides of tiled operands are not checked
     assert lib.dkv_linear_tiled(ok, 0, ok, 0, 0, 960, 960, None, 1e-5, 0, None, 0, ok, 0, 7, None) == 0
+    assert lib.dkv_linear_tiled(ok, 0, ok, 0, 0, 960, 960, None, 1e-5, 1, ok, 0, ok, 0, 15, None) == 0

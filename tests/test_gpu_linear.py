@@ -120,6 +120,10 @@ def test_tiled_layouts_equal_row_major(cuda, rows, k, n, norm, epi):
         got = gpu_ops.linear(x, w, weight_tiled=wt, out_tiled=True, **kw)
         assert got.shape == ((rows + 15) // 16 * 16, n_out)
         assert torch.equal(gpu_ops.mfma_untiled(got, rows), want)
+        if res is not None:  # a tiled residual too
+            kw['residual'] = gpu_ops.mfma_tiled(res)
+            got = gpu_ops.linear(xt, w, weight_tiled=wt, x_tiled=True, rows=rows, residual_tiled=True, **kw)
+            assert torch.equal(got, want)
     torch.cuda.synchronize()
 
 
