@@ -7,7 +7,8 @@ Also reported on the same line: frame-chunk attention (15 Q / 5 KV heads, 64-tok
 causal chunk over 1024/4096/8128-token mixed histories) in us/layer, GB/s and TFLOP/s;
 candidate scoring (4 continuations of 8-24 tokens over a 6144-token 4-bit / 8-bit
 history); the same attention workloads as independent launches in flight together over 8
-streams (`--only tput`: what the kernels sustain once launch latency overlaps); and the
+streams (`--only tput`: what the kernels sustain once launch latency overlaps); the decoder's
+projections as chains of dependent launches, row-major and MFMA-tiled (`--only linear`); and the
 reference CPU path timed on this host (the oracle restatement). The headline pack leg runs first;
 the end-to-end decoder and the 8-stream throughput leg each run in a fresh child process (the
 decoder's pipelined replays are 20% slower in a process that has run the other legs first).
@@ -17,7 +18,8 @@ memory per rotation (attention: as many distinct per-layer histories as that tak
 two copies of the volume, alternated), so the bytes come from HBM. The launch floor (a graph
 of tiny dependent kernels) is reported beside the attention numbers. The one exception is the
 reference's own attention microbenchmark (`--only ref`), replayed as the reference runs it (one
-cache-resident history, eager calls) so that its published times compare like for like.
+cache-resident history, eager calls) so that its published times compare like for like,
+and the projection chains of `--only linear` (see bench_linear).
 """
 import argparse
 import json
@@ -43,7 +45,8 @@ def parse():
     p.add_argument('--steps', type=int, default=200)
     p.add_argument('--warmup', type=int, default=20)
     p.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
-    p.add_argument('--only', choices=['pack', 'seg', 'attn', 'cand', 'ref', 'tput', 'e2e', 'all'], default='all')
+    p.add_argument('--only', choices=['pack', 'seg', 'attn', 'cand', 'ref', 'tput', 'e2e', 'linear', 'all'],
+                   default='all')
     p.add_argument('--rotate', type=int, default=48,
                    help='least number of distinct layers attention rotates over (more when the layers '
                         'hold less than 512 MB together)')
@@ -135,6 +138,62 @@ def graph_of(fn, reps):
             fn()
     torch.cuda.synchronize()
     return graph
+
+
+def bench_linear(layers=32, rows=64, reps=30):
+    """The decoder's four projections (960-wide, SwiGLU 2560, 15 / 5 heads) at `rows` rows, each as a
+    graph of `layers` dependent launches with distinct weights per layer (99, 59, 315 and 157 MB of
+    weights per chain for Q/K/V, o_proj, gate/up and down_proj: the chains under the 256 MB MALL
+    can keep part of their weights there between replays, which the decoder, streaming all four,
+    cannot): us per launch with row-major operands and with the MFMA-tiled ones the
+    fused decoder layer uses (tiled weights; gate/up reading a tiled h2 and writing SiLU*up tiled,
+    down_proj reading both tiled). Printed, and returned as a dict."""
+    import torch
+    from dkv import gpu_ops
+    dev, bf = torch.device('cuda:0'), torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(11)
+    H, I, QKV = 960, 2560, (15 + 2 * 5) * 64
+
+    def rnd(*shape, scale=1.0):
+        return (torch.randn(*shape, device=dev, generator=g) * scale).to(bf)
+    x, xi, res = rnd(rows, H, scale=0.5), rnd(rows, I, scale=0.5), rnd(rows, H)
+    norm = (1 + 0.1 * torch.randn(H, device=dev, generator=g)).to(bf)
+    w = dict(qkv=[rnd(QKV, H, scale=0.03) for _ in range(layers)], o=[rnd(H, H, scale=0.03) for _ in range(layers)],
+             gu=[rnd(2 * I, H, scale=0.03) for _ in range(layers)], d=[rnd(H, I, scale=0.02) for _ in range(layers)])
+    t = {k: [gpu_ops.mfma_tiled(m) for m in v] for k, v in w.items()}
+    xt, xit, rt = gpu_ops.mfma_tiled(x), gpu_ops.mfma_tiled(xi), gpu_ops.mfma_tiled(res)
+    L = gpu_ops.linear
+    chains = {
+        'qkv': (lambda: [L(x, m, norm=norm) for m in w['qkv']],
+                lambda: [L(x, m, norm=norm, weight_tiled=mt) for m, mt in zip(w['qkv'], t['qkv'])]),
+        'o_proj': (lambda: [L(x, m, residual=res) for m in w['o']],
+                   lambda: [L(x, m, residual=res, weight_tiled=mt, out_tiled=True) for m, mt in zip(w['o'], t['o'])]),
+        'gate_up': (lambda: [L(x, m, norm=norm, silu_mul=True) for m in w['gu']],
+                    lambda: [L(xt, m, norm=norm, silu_mul=True, weight_tiled=mt, x_tiled=True, rows=rows,
+                               out_tiled=True) for m, mt in zip(w['gu'], t['gu'])]),
+        'down_proj': (lambda: [L(xi, m, residual=res) for m in w['d']],
+                      lambda: [L(xit, m, residual=rt, weight_tiled=mt, x_tiled=True, rows=rows, residual_tiled=True)
+                               for m, mt in zip(w['d'], t['d'])]),
+    }
+    out = {}
+    for name, fns in chains.items():
+        us = []
+        for fn in fns:
+            graph = graph_of(fn, 1)
+            for _ in range(20):
+                graph.replay()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(reps):
+                graph.replay()
+            b.record()
+            b.synchronize()
+            us.append(a.elapsed_time(b) / reps / layers * 1e3)
+        out[name] = dict(row_major_us=us[0], tiled_us=us[1])
+        print(f'# linear {name} ({rows} rows, {layers} dependent launches): {us[0]:.2f} us per launch row-major, '
+              f'{us[1]:.2f} tiled', flush=True)
+    return out
 
 
 def bench_pack(steps, warmup, reps=10):
@@ -730,6 +789,8 @@ def main():
         res['e2e'] = bench_e2e()
     elif args.only == 'all':
         res['e2e'] = leg_in_child(args, 'e2e', 'e2e')
+    if args.only == 'linear':
+        res['linear'] = bench_linear()
     if args.only == 'tput':
         res['throughput'] = bench_throughput(args.steps, args.warmup, args.rotate)
     elif args.only == 'all':
@@ -780,6 +841,10 @@ def main():
                for k, r in res['throughput'].items() if k != 'workload'})
     if 'e2e' in res:
         line['e2e'] = res['e2e']
+    if 'linear' in res:
+        line['linear'] = dict(workload='decoder projections at 64 rows, 32 dependent launches per graph, weights '
+                                       'from HBM; us per launch', **{k: {kk: round(vv, 3) for kk, vv in r.items()}
+                                                                    for k, r in res['linear'].items()})
     if cpu:
         main_threads = str(cpu['cores'])
         line['cpu_baseline'] = dict(
